@@ -1,0 +1,202 @@
+#!/usr/bin/env python3
+"""Benchmark of the paged-attention decode hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--variant v2|v1]
+                    [--partition P] [--rotate R] [--no-cpu]
+
+Workload: Llama-3-8B layer decode (32 query heads, 8 kv heads, head_dim 128,
+block_size 16, batch 64, context lengths uniform in [512, 4096], randomly
+permuted block tables over a pool of 1.25x the blocks needed, fp16 values
+~ N(0, 0.5)). A step is one decode call over that batch with every input
+already resident in HBM. R copies of the KV pool (default 4, ~3 GB) are
+rotated between calls so no call finds its 604 MB of K/V in the 256 MB
+Infinity Cache.
+
+Prints one JSON line: the metric (KV-read GB/s), us/call, the roofline of the
+decode kernel (algorithmic bytes / kernel time vs the 8 TB/s HBM peak) and the
+fp32 CPU restatement timed on this host as a reference point.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--variant", choices=["v1", "v2"], default="v2")
+    ap.add_argument("--partition", type=int, default=256)
+    ap.add_argument("--rotate", type=int, default=4)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--samples", type=int, default=200, help="launches timed one by one for p10/p50/p90")
+    return ap.parse_args()
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE={world}); the path has no multi-GPU mode.", file=sys.stderr)
+        sys.exit(2)
+
+    from swiftllm_amd import _hip, workloads
+    from swiftllm_amd import paged_attention as pa
+    from swiftllm_amd._hip import DeviceArray, Event, Stream
+
+    if _hip.device_count() < 1:
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        sys.exit(1)
+
+    t0 = time.time()
+    w = workloads.decode_config(2, seed=args.seed)
+    sh = w.shape
+    kv_bytes = w.kv_bytes()
+    alg_bytes = kv_bytes + w.other_bytes()
+    print(f"[bench] workload generated in {time.time() - t0:.1f}s: S={sh['num_seqs']} "
+          f"sum(ctx)={int(w.context_lens.sum())} pool={sh['num_blocks']} blocks "
+          f"kv_bytes={kv_bytes / 1e6:.1f} MB", file=sys.stderr, flush=True)
+
+    stream = Stream()
+    q = DeviceArray.from_numpy(w.q)
+    bt = DeviceArray.from_numpy(w.block_tables)
+    ctx = DeviceArray.from_numpy(w.context_lens)
+    out = DeviceArray(w.q.shape, np.float16)
+    pools = [(DeviceArray.from_numpy(w.key_cache), DeviceArray.from_numpy(w.value_cache))
+             for _ in range(max(1, args.rotate))]
+    ws = None
+    if args.variant == "v2":
+        ws = pa.workspace(pa.paged_attention_v2_workspace_size(
+            sh["num_seqs"], sh["num_heads"], sh["num_kv_heads"], sh["head_dim"], sh["block_size"],
+            sh["max_num_blocks_per_seq"], args.partition), stream)
+
+    def step(i):
+        kc, vc = pools[i % len(pools)]
+        if args.variant == "v2":
+            pa.paged_attention_v2(out, ws, q, kc, vc, bt, ctx, w.scale, sh["num_seqs"],
+                                  sh["num_heads"], sh["num_kv_heads"], sh["head_dim"],
+                                  sh["block_size"], sh["max_num_blocks_per_seq"], args.partition,
+                                  num_blocks=sh["num_blocks"], stream=stream)
+        else:
+            pa.paged_attention_v1(out, q, kc, vc, bt, ctx, w.scale, sh["num_seqs"],
+                                  sh["num_heads"], sh["num_kv_heads"], sh["head_dim"],
+                                  sh["block_size"], sh["max_num_blocks_per_seq"],
+                                  num_blocks=sh["num_blocks"], stream=stream)
+
+    for i in range(args.warmup):
+        step(i)
+    stream.synchronize()
+    print(f"[bench] warmup {args.warmup} done", file=sys.stderr, flush=True)
+
+    # Timed region: K back-to-back launches on one stream between two events.
+    start, end = Event(), Event()
+    _hip.synchronize()
+    start.record(stream)
+    for i in range(args.steps):
+        step(i)
+    end.record(stream)
+    end.synchronize()
+    _hip.synchronize()
+    total_ms = start.elapsed_ms(end)
+    ms = total_ms / args.steps
+    print(f"[bench] timed {args.steps} steps: {ms * 1e3:.2f} us/call", file=sys.stderr, flush=True)
+
+    # Per-launch distribution: each launch bracketed by its own events.
+    per = []
+    evs = [(Event(), Event()) for _ in range(args.samples)]
+    for i, (a, b) in enumerate(evs):
+        a.record(stream)
+        step(i)
+        b.record(stream)
+    stream.synchronize()
+    per = np.array([a.elapsed_ms(b) * 1e3 for a, b in evs]) if evs else np.array([ms * 1e3])
+    p10, p50, p90 = (float(np.percentile(per, x)) for x in (10, 50, 90))
+
+    value = kv_bytes / (ms * 1e-3) / 1e9          # KV-read GB/s
+    achieved = alg_bytes / (ms * 1e-3) / 1e9      # all algorithmic bytes / kernel time
+
+    traffic = None
+    tf = ROOT / "profiles" / "decode_config2_traffic.json"
+    if tf.exists():
+        try:
+            traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
+        except Exception:
+            traffic = None
+
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+
+        threads = oracle.lib().oracle_max_threads()
+        oracle.decode_f32(w.q, w.key_cache, w.value_cache, w.block_tables, w.context_lens, w.scale)
+        times = []
+        t_budget = time.time()
+        while len(times) < 5 and (time.time() - t_budget) < 20.0:
+            t1 = time.perf_counter()
+            oracle.decode_f32(w.q, w.key_cache, w.value_cache, w.block_tables, w.context_lens, w.scale)
+            times.append(time.perf_counter() - t1)
+        cpu_s = float(np.median(times))
+        cpu = {"value": round(kv_bytes / cpu_s / 1e9, 3), "unit": "GB/s", "cores": int(threads),
+               "kind": "port", "us_per_call": round(cpu_s * 1e6, 1),
+               "sample": f"full config-2 batch (same inputs), fp32 C restatement "
+                         f"(oracle/oracle.c, OpenMP over (seq, kv head)), median of {len(times)} runs"}
+        print(f"[bench] cpu baseline {cpu_s * 1e3:.1f} ms/call on {threads} threads", file=sys.stderr,
+              flush=True)
+
+    rec = {
+        "metric": "paged-attn decode KV-read GB/s (% HBM peak) + us/call @ Llama-3-8B shape",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "us_per_call": round(ms * 1e3, 3),
+        "us_per_call_p10_p50_p90": [round(p10, 2), round(p50, 2), round(p90, 2)],
+        "hbm_peak_frac": round(value / HBM_PEAK_GBS, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 in/out, f32 accumulate",
+        "data": "synthetic (seeded N(0,0.5) fp16, random permuted block tables)",
+        "config": {
+            "workload": "llama3-8b-decode-layer",
+            "num_seqs": sh["num_seqs"], "num_heads": sh["num_heads"],
+            "num_kv_heads": sh["num_kv_heads"], "head_dim": sh["head_dim"],
+            "block_size": sh["block_size"], "context_lens": "uniform[512,4096]",
+            "sum_context": int(w.context_lens.sum()), "pool_blocks": sh["num_blocks"],
+            "kernel": f"paged_attention_{args.variant}" + (f"/partition{args.partition}" if args.variant == "v2" else ""),
+            "kv_pool_copies_rotated": len(pools), "seed": args.seed,
+            "kv_bytes_per_call": kv_bytes, "algorithmic_bytes_per_call": alg_bytes,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

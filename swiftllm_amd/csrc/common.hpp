@@ -1,0 +1,62 @@
+// Shared helpers for the gfx950 kernels and their C-ABI launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "swiftllm_hip.h"
+
+namespace swiftllm {
+
+using f16 = _Float16;
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// Host-side status reporting (abi.cpp). Every exported entry point ends in
+// ok() or fail(); the void launchers leave the result in the thread-local
+// slot read by swiftllm_hip_last_error().
+// ---------------------------------------------------------------------------
+int ok();
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// SWIFTLLM_OK when a HIP device is visible, else SWIFTLLM_ERR_DEVICE_NOT_FOUND.
+int require_device();
+// Maps the result of hipLaunchKernel to a status.
+int launched(hipError_t err, const char* what);
+
+inline bool aligned(const void* p, size_t bytes) {
+    return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
+}
+
+// Launches `kernel(args)` where the kernel takes one by-value argument
+// struct; returns the HIP error of the launch itself.
+template <typename Args>
+hipError_t launch(void (*kernel)(Args), dim3 grid, dim3 block, size_t lds,
+                  hipStream_t stream, const Args& args) {
+    void* argv[] = {const_cast<Args*>(&args)};
+    return hipLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block,
+                           argv, lds, stream);
+}
+
+// ---------------------------------------------------------------------------
+// KV-cache addressing, layout [num_blocks, num_kv_heads, head_dim, 16]
+// (paged_attention.cu:39-40, 85-87, 114-116). One (block, kv head) pair is a
+// contiguous tile of head_dim rows of 16 tokens.
+// ---------------------------------------------------------------------------
+constexpr int kBlockTokens = 16;
+
+__host__ __device__ inline size_t kv_tile_offset(int block, int kv_head,
+                                                 int num_kv_heads,
+                                                 int head_dim) {
+    return (static_cast<size_t>(block) * num_kv_heads + kv_head) *
+           static_cast<size_t>(head_dim) * kBlockTokens;
+}
+
+// Element (d, t) of a tile.
+__host__ __device__ inline int kv_elem_offset(int d, int t) {
+    return d * kBlockTokens + t;
+}
+
+}  // namespace swiftllm

@@ -1,0 +1,778 @@
+// Paged-attention decode for gfx950 (CDNA4).
+//
+// Contract (paged_attention.cu:35-137 is the reference's text; its output
+// stage is a stub, so the behaviour below is the textbook attention its
+// comments and indexing describe):
+//   for sequence s, query head h, kv head kvh = h / (H / Hkv)   (cu:52)
+//   L = context_lens[s]; token j lives in block bt[s, j / 16] at offset j % 16
+//   logit_j = scale * sum_d q[s,h,d] * K(b, kvh, d, j % 16)     (cu:92-96)
+//   out[s,h,:] = sum_j softmax(logit)_j * V(b, kvh, :, j % 16)  (cu:113-135)
+// fp16 in and out, fp32 accumulation; L <= 0 writes zeros.
+//
+// Work decomposition. One workgroup serves every query head of one kv head
+// (up to 16 per workgroup), so each K/V tile is read from HBM once. The
+// reference grid (S, H) (cu:248) re-reads it H/Hkv times. The waves of a
+// workgroup take the blocks of its token range round-robin; the range is the
+// whole context (single pass) or one partition of it (split-K). Each wave
+// keeps a running max, sum and output for its blocks; the waves merge through
+// LDS. Split-K partitions leave (max, sum, output) in a workspace and a
+// second kernel does the rescaled reduce (the kernel boundary makes the
+// partials visible; an in-kernel last-arriver reduce would need device-scope
+// fences, which write back and invalidate the whole L2 on this GPU).
+//
+// Per 16-token block, each wave runs the whole computation on the matrix
+// cores with v_mfma_f32_16x16x16_f16 (the group of query heads is the N = 16
+// side, zero-padded):
+//   1. K tile rows 16J..16J+15 arrive with tokens contiguous ([d][t]); an
+//      MFMA against a 0/1 identity operand returns the same values in the
+//      transposed ([t][d]) register layout, exactly (one product per output).
+//   2. S^T[t][g] = sum_d K^T[t][d] Q^T[d][g]          (D/16 MFMAs)
+//   3. Online softmax in fp32 on the S^T accumulator; the 4 token rows of a
+//      head live in lanes l, l^16, l^32, l^48, so the block max is two xor
+//      shuffles.
+//   4. O^T[d][g] += V[d][t] P^T[t][g] with V in its stored layout. P is fed as
+//      an fp16 hi part plus an fp16 lo part (two MFMAs), which keeps ~22 bits
+//      of each probability; P is computed as 2^15 * exp2(s - m) so both parts
+//      stay in fp16's normal range.
+
+#include <algorithm>
+#include <cmath>
+
+#include "common.hpp"
+
+namespace swiftllm {
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+// Probabilities are produced as 2^kPExp * exp2(s - m) (<= 2^15 < 65504).
+constexpr float kPExp = 15.0f;
+
+struct DecodeArgs {
+    f16* out;
+    const f16* q;
+    const f16* kc;
+    const f16* vc;
+    const int* bt;
+    const int* ctx;
+    float* ws_max;       // [S][H][MP]         log2-domain max logit
+    float* ws_sum;       // [S][H][MP]         sum of 2^15 * exp2(s - max)
+    float* ws_out;       // [S][H][MP][D]      normalised partial output
+    float scale_log2;    // scale * log2(e)
+    int H;
+    int Hkv;
+    int G;            // query heads per kv head
+    int nhc;          // head chunks of 16 per kv head
+    int MB;           // max_num_blocks_per_seq (row stride of bt)
+    int num_blocks;   // bound on block ids; <= 0: unbounded
+    int part_blocks;  // blocks per partition; 0: single pass
+    int MP;           // partitions per sequence in the workspace
+};
+
+__device__ __forceinline__ f4 mfma16(h4 a, h4 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ h4 mask_h4(h4 v, unsigned long long m) {
+    return __builtin_bit_cast(h4, __builtin_bit_cast(unsigned long long, v) & m);
+}
+
+__device__ __forceinline__ h4 to_h4(f4 v) {
+    h4 r;
+    r[0] = static_cast<f16>(v[0]);
+    r[1] = static_cast<f16>(v[1]);
+    r[2] = static_cast<f16>(v[2]);
+    r[3] = static_cast<f16>(v[3]);
+    return r;
+}
+
+__device__ __forceinline__ bool block_ok(int b, int num_blocks) {
+    return num_blocks <= 0 || static_cast<unsigned>(b) < static_cast<unsigned>(num_blocks);
+}
+
+template <int D>
+__device__ __forceinline__ void load_tile(const DecodeArgs& a, int b, int kvh,
+                                          int loff, h4 (&k)[D / 16],
+                                          h4 (&v)[D / 16]) {
+    constexpr int NJ = D / 16;
+    // An id outside the pool reads block 0 instead (in bounds); the caller
+    // skips such a block.
+    const int bsafe = block_ok(b, a.num_blocks) ? b : 0;
+    const size_t base = kv_tile_offset(bsafe, kvh, a.Hkv, D) + loff;
+    const f16* kp = a.kc + base;
+    const f16* vp = a.vc + base;
+#pragma unroll
+    for (int J = 0; J < NJ; ++J) {
+        k[J] = *reinterpret_cast<const h4*>(kp + kv_elem_offset(16 * J, 0));
+    }
+#pragma unroll
+    for (int J = 0; J < NJ; ++J) {
+        v[J] = *reinterpret_cast<const h4*>(vp + kv_elem_offset(16 * J, 0));
+    }
+}
+
+// Running softmax state of one wave: max (log2 domain), sum of
+// 2^15 * exp2(s - max) over this lane's token rows, and O^T accumulators.
+template <int D>
+struct WaveState {
+    float m;
+    float l;
+    f4 acc[D / 16];
+};
+
+// Steps 1-4 of the header for one block whose first nv tokens are valid
+// (nv == 0: the block contributes nothing).
+template <int D>
+__device__ __forceinline__ void attend_block(WaveState<D>& st, int nv, int kg,
+                                             h4 (&kA)[D / 16], h4 (&vA)[D / 16],
+                                             const h4 (&qB)[D / 16], h4 ident,
+                                             float scale_log2) {
+    constexpr int NJ = D / 16;
+    if (nv < kBlockTokens) {
+        // Tail block: zero the K/V of tokens past the context so no stale
+        // value (possibly NaN) reaches a sum through a 0 weight.
+        const int c = min(max(nv - 4 * kg, 0), 4);
+        const unsigned long long m = (c >= 4) ? ~0ull : ((1ull << (16 * c)) - 1ull);
+#pragma unroll
+        for (int J = 0; J < NJ; ++J) {
+            kA[J] = mask_h4(kA[J], m);
+            vA[J] = mask_h4(vA[J], m);
+        }
+    }
+    // Steps 1 + 2.
+    f4 s0 = f4{0, 0, 0, 0}, s1 = f4{0, 0, 0, 0};
+#pragma unroll
+    for (int J = 0; J < NJ; ++J) {
+        const f4 t = mfma16(kA[J], ident, f4{0, 0, 0, 0});
+        const h4 kT = to_h4(t);
+        if (J & 1) {
+            s1 = mfma16(kT, qB[J], s1);
+        } else {
+            s0 = mfma16(kT, qB[J], s0);
+        }
+    }
+    // Step 3. Lane (r, kg) holds S^T[t = 4kg + i][g = r].
+    float sv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        sv[i] = (s0[i] + s1[i]) * scale_log2;
+        if (4 * kg + i >= nv) sv[i] = -INFINITY;
+    }
+    float bm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    bm = fmaxf(bm, __shfl_xor(bm, 16));
+    bm = fmaxf(bm, __shfl_xor(bm, 32));
+    if (__any(bm > st.m)) {
+        const float m_new = fmaxf(st.m, bm);
+        const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
+#pragma unroll
+        for (int J = 0; J < NJ; ++J) st.acc[J] *= alpha;
+        st.l *= alpha;
+        st.m = m_new;
+    }
+    // While no valid token has been seen (an out-of-pool block, nv == 0) the
+    // max is still -inf and every sv is -inf: use 0 so the weights are 0.
+    const float m_use = (st.m == -INFINITY) ? 0.0f : st.m;
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(sv[i] - m_use + kPExp);
+    st.l += (p[0] + p[1]) + (p[2] + p[3]);
+    h4 ph, pl;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        ph[i] = static_cast<f16>(p[i]);
+        pl[i] = static_cast<f16>(p[i] - static_cast<float>(ph[i]));
+    }
+    // Step 4. Lane (r, kg) accumulates O^T[d = 16J + 4kg + i][g = r].
+#pragma unroll
+    for (int J = 0; J < NJ; ++J) {
+        st.acc[J] = mfma16(vA[J], ph, st.acc[J]);
+        st.acc[J] = mfma16(vA[J], pl, st.acc[J]);
+    }
+}
+
+// Longest-first dispatch: workgroups are issued roughly in blockIdx order, so
+// blockIdx.z = r serves the sequence with the r-th longest context (ties by
+// index). Long sequences start first and short ones fill in at the end.
+// Sequence counts above kLptMaxSeqs keep the identity order (the O(S^2)
+// ranking below would cost more than it saves).
+#ifndef SWIFTLLM_LPT_MAX_SEQS
+#define SWIFTLLM_LPT_MAX_SEQS 1024
+#endif
+constexpr int kLptMaxSeqs = SWIFTLLM_LPT_MAX_SEQS;
+
+__device__ __forceinline__ int sequence_for_block(const int* ctx, int S, int r) {
+    if (S > kLptMaxSeqs) return r;
+    __shared__ int s_seq;
+    if (threadIdx.x == 0) s_seq = r;
+    __syncthreads();
+    for (int c = threadIdx.x; c < S; c += blockDim.x) {
+        const int lc = ctx[c];
+        int rank = 0;
+        for (int o = 0; o < S; ++o) {
+            const int lo = ctx[o];
+            rank += (lo > lc) || (lo == lc && o < c);
+        }
+        if (rank == r) s_seq = c;
+    }
+    __syncthreads();
+    return s_seq;
+}
+
+template <int D, int NW>
+__global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeArgs a) {
+    constexpr int NJ = D / 16;
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15;   // MFMA column / row-in-slice index
+    const int kg = lane >> 4;  // MFMA k-group: 4 consecutive k per lane
+
+    const int part = blockIdx.x;
+    const int kvh = blockIdx.y / a.nhc;
+    const int hc = blockIdx.y - kvh * a.nhc;
+    const int s = sequence_for_block(a.ctx, gridDim.z, blockIdx.z);
+    const int g0 = hc * 16;
+    const int gn = min(16, a.G - g0);  // query heads served here
+    const int gstride = min(16, a.G);  // LDS rows per wave
+    const int h0 = kvh * a.G + g0;
+
+    int L = a.ctx[s];
+    L = max(L, 0);
+    const int nblk = min((L + kBlockTokens - 1) / kBlockTokens, a.MB);
+    L = min(L, nblk * kBlockTokens);
+    int nparts, jb0, jb1;
+    if (a.part_blocks > 0) {
+        nparts = (nblk + a.part_blocks - 1) / a.part_blocks;
+        jb0 = part * a.part_blocks;
+        jb1 = min(nblk, jb0 + a.part_blocks);
+    } else {
+        nparts = 1;
+        jb0 = 0;
+        jb1 = nblk;
+    }
+    if (nblk == 0) {
+        if (part == 0) {
+            for (int i = threadIdx.x; i < gn * D; i += NW * 64) {
+                a.out[(static_cast<size_t>(s) * a.H + h0) * D + i] = static_cast<f16>(0.0f);
+            }
+        }
+        return;
+    }
+    if (part >= nparts) return;
+
+    // Q^T operand of step 2: lane (r, kg) holds q[h0 + r][16J + 4kg .. +3].
+    h4 qB[NJ];
+    {
+        const f16* qp = a.q + (static_cast<size_t>(s) * a.H + h0 + min(r, gn - 1)) * D + 4 * kg;
+#pragma unroll
+        for (int J = 0; J < NJ; ++J) {
+            const h4 v = *reinterpret_cast<const h4*>(qp + 16 * J);
+            qB[J] = (r < gn) ? v : h4{0, 0, 0, 0};
+        }
+    }
+    // Identity operand of step 1: B[k = 4kg + i][n = r] = (k == n).
+    h4 ident;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        ident[i] = (4 * kg + i == r) ? static_cast<f16>(1.0f) : static_cast<f16>(0.0f);
+    }
+    // Lane (r, kg) loads tile row 16J + r, tokens 4kg .. 4kg + 3.
+    const int loff = kv_elem_offset(r, 4 * kg);
+    const int* btrow = a.bt + static_cast<size_t>(s) * a.MB;
+
+    WaveState<D> st;
+    st.m = -INFINITY;
+    st.l = 0.0f;
+#pragma unroll
+    for (int J = 0; J < NJ; ++J) st.acc[J] = f4{0, 0, 0, 0};
+
+    // Blocks jb0 + w, jb0 + w + NW, ... of this wave, double-buffered in
+    // registers: the next block's loads are in flight while one is computed.
+    // Two blocks per iteration with every load and every attend_block
+    // unconditional, so all paths have the same loads in flight and the
+    // compiler's wait counts stay exact. Past the wave's last block the
+    // prefetch reloads the current tile (a cache hit) and the odd tail is
+    // attended with nv = 0.
+    const int first = jb0 + w;
+    const int nbw = (jb1 > first) ? (jb1 - first + NW - 1) / NW : 0;
+    if (nbw > 0) {
+        h4 kA[NJ], vA[NJ], kB[NJ], vB[NJ];
+        const int last = first + (nbw - 1) * NW;
+        int bA = __builtin_amdgcn_readfirstlane(btrow[first]);
+        load_tile<D>(a, bA, kvh, loff, kA, vA);
+        for (int i = 0; i < nbw; i += 2) {
+            const int jA = first + i * NW;
+            const int jB = jA + NW;
+            const int jC = jB + NW;
+            const int bB = __builtin_amdgcn_readfirstlane(btrow[min(jB, last)]);
+            load_tile<D>(a, bB, kvh, loff, kB, vB);
+            attend_block<D>(st, block_ok(bA, a.num_blocks) ? min(kBlockTokens, L - jA * kBlockTokens) : 0,
+                            kg, kA, vA, qB, ident, a.scale_log2);
+            bA = __builtin_amdgcn_readfirstlane(btrow[min(jC, last)]);
+            load_tile<D>(a, bA, kvh, loff, kA, vA);
+            attend_block<D>(st,
+                            (jB <= last && block_ok(bB, a.num_blocks)) ? min(kBlockTokens, L - jB * kBlockTokens) : 0,
+                            kg, kB, vB, qB, ident, a.scale_log2);
+        }
+    }
+    float m_run = st.m;
+    float l_run = st.l;
+    f4 (&acc)[NJ] = st.acc;
+    // Per-lane partial sums cover tokens 4kg..4kg+3 of every block.
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
+
+    // Merge the waves of this workgroup.
+    extern __shared__ __align__(16) float smem[];
+    float* sm_m = smem;            // [NW][16]
+    float* sm_l = smem + NW * 16;  // [NW][16]
+    float* sm_o = smem + NW * 32;  // [NW][gstride][D]
+    if (kg == 0) {
+        sm_m[w * 16 + r] = m_run;
+        sm_l[w * 16 + r] = l_run;
+    }
+    if (r < gn) {
+#pragma unroll
+        for (int J = 0; J < NJ; ++J) {
+            *reinterpret_cast<f4*>(sm_o + static_cast<size_t>(w * gstride + r) * D + 16 * J + 4 * kg) = acc[J];
+        }
+    }
+    __syncthreads();
+
+    const bool direct = (nparts == 1);
+    for (int idx = threadIdx.x; idx < gn * D; idx += NW * 64) {
+        const int g = idx / D;
+        const int d = idx - g * D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w2 = 0; w2 < NW; ++w2) M = fmaxf(M, sm_m[w2 * 16 + g]);
+        float num = 0.0f, den = 0.0f;
+#pragma unroll
+        for (int w2 = 0; w2 < NW; ++w2) {
+            const float mw = sm_m[w2 * 16 + g];
+            const float f = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+            num += f * sm_o[static_cast<size_t>(w2 * gstride + g) * D + d];
+            den += f * sm_l[w2 * 16 + g];
+        }
+        const int h = h0 + g;
+        const float o = (den > 0.0f) ? num / den : 0.0f;
+        if (direct) {
+            a.out[(static_cast<size_t>(s) * a.H + h) * D + d] = static_cast<f16>(o);
+        } else {
+            const size_t pi = (static_cast<size_t>(s) * a.H + h) * a.MP + part;
+            a.ws_out[pi * D + d] = o;
+            if (d == 0) {
+                a.ws_max[pi] = M;
+                a.ws_sum[pi] = den;
+            }
+        }
+    }
+}
+
+// Split-K reduce: one workgroup per (sequence, kv head, head chunk) with more
+// than one partition; partition p contributes exp2(m_p - M) * l_p * o_p.
+struct ReduceArgs {
+    f16* out;
+    const int* ctx;
+    const float* ws_max;
+    const float* ws_sum;
+    const float* ws_out;
+    int H;
+    int G;
+    int nhc;
+    int MB;
+    int part_blocks;
+    int MP;
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void paged_reduce_kernel(const ReduceArgs a) {
+    const int kvh = blockIdx.x / a.nhc;
+    const int hc = blockIdx.x - kvh * a.nhc;
+    const int s = blockIdx.y;
+    const int g0 = hc * 16;
+    const int gn = min(16, a.G - g0);
+    const int h0 = kvh * a.G + g0;
+    const int L = max(a.ctx[s], 0);
+    const int nblk = min((L + kBlockTokens - 1) / kBlockTokens, a.MB);
+    const int nparts = (nblk + a.part_blocks - 1) / a.part_blocks;
+    if (nparts <= 1) return;  // written directly by the partition kernel
+    for (int idx = threadIdx.x; idx < gn * D; idx += blockDim.x) {
+        const int g = idx / D;
+        const int d = idx - g * D;
+        const int h = h0 + g;
+        const size_t base = (static_cast<size_t>(s) * a.H + h) * a.MP;
+        float M = -INFINITY;
+        for (int p = 0; p < nparts; ++p) M = fmaxf(M, a.ws_max[base + p]);
+        float num = 0.0f, den = 0.0f;
+        for (int p = 0; p < nparts; ++p) {
+            const float mp = a.ws_max[base + p];
+            const float f = (mp == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mp - M) * a.ws_sum[base + p];
+            num += f * a.ws_out[(base + p) * D + d];
+            den += f;
+        }
+        a.out[(static_cast<size_t>(s) * a.H + h) * D + d] = static_cast<f16>(den > 0.0f ? num / den : 0.0f);
+    }
+}
+
+// Bit-exact materialisation of one (sequence, kv head) through the tile
+// addressing above.
+struct GatherArgs {
+    const uint16_t* kc;
+    const uint16_t* vc;
+    const int* bt;
+    const int* ctx;
+    uint16_t* ko;
+    uint16_t* vo;
+    int s, kvh, Hkv, D, MB, max_len;
+};
+
+__global__ __launch_bounds__(256) void gather_kv_kernel(const GatherArgs a) {
+    int L = max(a.ctx[a.s], 0);
+    L = min(L, min(a.MB * kBlockTokens, a.max_len));
+    const int* btrow = a.bt + static_cast<size_t>(a.s) * a.MB;
+    const size_t n = static_cast<size_t>(a.max_len) * a.D;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        const int t = static_cast<int>(i / a.D);
+        const int d = static_cast<int>(i - static_cast<size_t>(t) * a.D);
+        uint16_t kv = 0, vv = 0;
+        if (t < L) {
+            const int b = btrow[t / kBlockTokens];
+            const size_t off = kv_tile_offset(b, a.kvh, a.Hkv, a.D) + kv_elem_offset(d, t % kBlockTokens);
+            kv = a.kc[off];
+            vv = a.vc[off];
+        }
+        a.ko[i] = kv;
+        a.vo[i] = vv;
+    }
+}
+
+struct ClearArgs {
+    uint32_t* p;
+    size_t words;
+};
+
+__global__ __launch_bounds__(256) void clear_kernel(const ClearArgs a) {
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < a.words;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        a.p[i] = 0u;
+    }
+}
+
+
+// ---------------------------------------------------------------------------
+// Host side.
+// ---------------------------------------------------------------------------
+constexpr size_t kAlign = 256;
+
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+struct Shape {
+    int S, H, Hkv, D, BS, MB;
+};
+
+int validate_decode(const char* who, const void* out, const void* q, const void* kc,
+                    const void* vc, const int* bt, const int* ctx, const Shape& sh) {
+    if (sh.S < 0 || sh.H <= 0 || sh.Hkv <= 0 || sh.MB < 0) {
+        return fail(SWIFTLLM_ERR_INVALID_PARAMETER,
+                    "%s: num_seqs=%d num_heads=%d num_kv_heads=%d max_num_blocks_per_seq=%d",
+                    who, sh.S, sh.H, sh.Hkv, sh.MB);
+    }
+    if (sh.H % sh.Hkv != 0) {
+        return fail(SWIFTLLM_ERR_INVALID_PARAMETER,
+                    "%s: num_heads %d is not a multiple of num_kv_heads %d", who, sh.H, sh.Hkv);
+    }
+    if (sh.D != 64 && sh.D != 128) {
+        return fail(SWIFTLLM_ERR_NOT_SUPPORTED, "%s: head_dim %d (supported: 64, 128)", who, sh.D);
+    }
+    if (sh.BS != kBlockTokens) {
+        return fail(SWIFTLLM_ERR_NOT_SUPPORTED, "%s: block_size %d (supported: 16)", who, sh.BS);
+    }
+    if (sh.S > 65535) {
+        return fail(SWIFTLLM_ERR_NOT_SUPPORTED, "%s: num_seqs %d > 65535", who, sh.S);
+    }
+    const long long nhc = (sh.H / sh.Hkv + 15) / 16;
+    if (static_cast<long long>(sh.Hkv) * nhc > 65535) {
+        return fail(SWIFTLLM_ERR_NOT_SUPPORTED, "%s: too many kv heads", who);
+    }
+    if (sh.S == 0) return SWIFTLLM_OK;
+    if (!out || !q || !kc || !vc || !bt || !ctx) {
+        return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: null pointer", who);
+    }
+    if (!aligned(out, 2) || !aligned(q, 8) || !aligned(kc, 8) || !aligned(vc, 8) ||
+        !aligned(bt, 4) || !aligned(ctx, 4)) {
+        return fail(SWIFTLLM_ERR_INVALID_PARAMETER,
+                    "%s: misaligned pointer (query and caches need 8-byte alignment)", who);
+    }
+    return SWIFTLLM_OK;
+}
+
+template <int D, int NW>
+hipError_t launch_decode_t(const DecodeArgs& a, int S, int mp_grid, hipStream_t stream) {
+    const int gstride = a.G < 16 ? a.G : 16;
+    const size_t lds = static_cast<size_t>(NW) * 32 * sizeof(float) +
+                       static_cast<size_t>(NW) * gstride * D * sizeof(float);
+    dim3 grid(mp_grid, a.Hkv * a.nhc, S);
+    return launch(paged_decode_kernel<D, NW>, grid, dim3(NW * 64), lds, stream, a);
+}
+
+hipError_t launch_decode(const DecodeArgs& a, int D, int NW, int S, int mp_grid,
+                         hipStream_t stream) {
+    if (D == 128) {
+        return NW == 16 ? launch_decode_t<128, 16>(a, S, mp_grid, stream)
+               : NW == 8 ? launch_decode_t<128, 8>(a, S, mp_grid, stream)
+                         : launch_decode_t<128, 4>(a, S, mp_grid, stream);
+    }
+    return NW == 16 ? launch_decode_t<64, 16>(a, S, mp_grid, stream)
+           : NW == 8 ? launch_decode_t<64, 8>(a, S, mp_grid, stream)
+                     : launch_decode_t<64, 4>(a, S, mp_grid, stream);
+}
+
+DecodeArgs make_args(void* out, const void* q, const void* kc, const void* vc, const int* bt,
+                     const int* ctx, float scale, const Shape& sh, int num_blocks) {
+    DecodeArgs a{};
+    a.out = static_cast<f16*>(out);
+    a.q = static_cast<const f16*>(q);
+    a.kc = static_cast<const f16*>(kc);
+    a.vc = static_cast<const f16*>(vc);
+    a.bt = bt;
+    a.ctx = ctx;
+    a.scale_log2 = static_cast<float>(static_cast<double>(scale) * static_cast<double>(kLog2e));
+    a.H = sh.H;
+    a.Hkv = sh.Hkv;
+    a.G = sh.H / sh.Hkv;
+    a.nhc = (a.G + 15) / 16;
+    a.MB = sh.MB;
+    a.num_blocks = num_blocks;
+    return a;
+}
+
+// Waves per workgroup of the single-pass kernel: the whole context of a
+// (sequence, kv head) is one workgroup, so it gets the most waves.
+#ifndef SWIFTLLM_WAVES_V1
+#define SWIFTLLM_WAVES_V1 8
+#endif
+constexpr int kWavesV1 = SWIFTLLM_WAVES_V1;
+// Waves per workgroup of a split-K partition.
+#ifndef SWIFTLLM_WAVES_V2
+#define SWIFTLLM_WAVES_V2 4
+#endif
+constexpr int kWavesV2 = SWIFTLLM_WAVES_V2;
+
+int decode_v1(void* out, const void* q, const void* kc, const void* vc, const int* bt,
+              const int* ctx, float scale, const Shape& sh, int num_blocks, hipStream_t stream,
+              const char* who) {
+    int rc = validate_decode(who, out, q, kc, vc, bt, ctx, sh);
+    if (rc != SWIFTLLM_OK) return rc;
+    if ((rc = require_device()) != SWIFTLLM_OK) return rc;
+    if (sh.S == 0) return ok();
+    DecodeArgs a = make_args(out, q, kc, vc, bt, ctx, scale, sh, num_blocks);
+    a.part_blocks = 0;
+    a.MP = 1;
+    return launched(launch_decode(a, sh.D, kWavesV1, sh.S, 1, stream), who);
+}
+
+// Split-K workspace: max logits and exp sums [S][H][MP] and partial outputs
+// [S][H][MP][D], all fp32. Plain scratch: every value a call reads was
+// written earlier in the same call, so it needs no initialisation.
+struct V2Need {
+    int MP;          // partitions per sequence
+    size_t stat;     // bytes of one [S][H][MP] float array
+    size_t total;    // bytes of the whole workspace
+};
+
+V2Need v2_need(const Shape& sh, int partition_size) {
+    V2Need n{};
+    const int part_blocks = partition_size / kBlockTokens;
+    n.MP = sh.MB == 0 ? 1 : (sh.MB + part_blocks - 1) / part_blocks;
+    n.stat = align_up(sizeof(float) * static_cast<size_t>(sh.S) * sh.H * n.MP);
+    n.total = 2 * n.stat + align_up(sizeof(float) * static_cast<size_t>(sh.S) * sh.H * n.MP * sh.D);
+    return n;
+}
+
+template <int D>
+hipError_t launch_reduce_t(const ReduceArgs& r, int S, int Hkv, hipStream_t stream) {
+    return launch(paged_reduce_kernel<D>, dim3(Hkv * r.nhc, S), dim3(256), 0, stream, r);
+}
+
+int validate_partition(const char* who, int partition_size) {
+    if (partition_size <= 0 || partition_size % kBlockTokens != 0) {
+        return fail(SWIFTLLM_ERR_INVALID_PARAMETER,
+                    "%s: partition_size %d must be a positive multiple of 16", who, partition_size);
+    }
+    return SWIFTLLM_OK;
+}
+
+int decode_v2(void* out, void* ws, size_t ws_bytes, const void* q, const void* kc, const void* vc,
+              const int* bt, const int* ctx, float scale, const Shape& sh, int partition_size,
+              int num_blocks, hipStream_t stream, const char* who) {
+    int rc = validate_decode(who, out, q, kc, vc, bt, ctx, sh);
+    if (rc != SWIFTLLM_OK) return rc;
+    if ((rc = validate_partition(who, partition_size)) != SWIFTLLM_OK) return rc;
+    const V2Need need = v2_need(sh, partition_size);
+    if (sh.S > 0) {
+        if (ws == nullptr || !aligned(ws, 256)) {
+            return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: workspace null or not 256-byte aligned", who);
+        }
+        if (ws_bytes < need.total) {
+            return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: workspace of %zu bytes, %zu needed", who,
+                        ws_bytes, need.total);
+        }
+    }
+    if ((rc = require_device()) != SWIFTLLM_OK) return rc;
+    if (sh.S == 0) return ok();
+    DecodeArgs a = make_args(out, q, kc, vc, bt, ctx, scale, sh, num_blocks);
+    char* base = static_cast<char*>(ws);
+    a.ws_max = reinterpret_cast<float*>(base);
+    a.ws_sum = reinterpret_cast<float*>(base + need.stat);
+    a.ws_out = reinterpret_cast<float*>(base + 2 * need.stat);
+    a.part_blocks = partition_size / kBlockTokens;
+    a.MP = need.MP;
+    hipError_t err = launch_decode(a, sh.D, kWavesV2, sh.S, need.MP, stream);
+    if (err != hipSuccess || need.MP <= 1) return launched(err, who);
+    ReduceArgs r{};
+    r.out = a.out;
+    r.ctx = ctx;
+    r.ws_max = a.ws_max;
+    r.ws_sum = a.ws_sum;
+    r.ws_out = a.ws_out;
+    r.H = a.H;
+    r.G = a.G;
+    r.nhc = a.nhc;
+    r.MB = a.MB;
+    r.part_blocks = a.part_blocks;
+    r.MP = a.MP;
+    err = sh.D == 128 ? launch_reduce_t<128>(r, sh.S, sh.Hkv, stream)
+                      : launch_reduce_t<64>(r, sh.S, sh.Hkv, stream);
+    return launched(err, who);
+}
+
+}  // namespace
+}  // namespace swiftllm
+
+using namespace swiftllm;
+
+extern "C" {
+
+void launch_paged_attention_v1(void* output, void* query, void* key_cache, void* value_cache,
+                               int* block_tables, int* context_lens, float scale, int num_seqs,
+                               int num_heads, int num_kv_heads, int head_dim, int block_size,
+                               int max_num_blocks_per_seq, hipStream_t stream) {
+    const Shape sh{num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_num_blocks_per_seq};
+    decode_v1(output, query, key_cache, value_cache, block_tables, context_lens, scale, sh, 0,
+              stream, "launch_paged_attention_v1");
+}
+
+int swiftllm_hip_launch_paged_attention_v1(void* output, const void* query, const void* key_cache,
+                                           const void* value_cache, const int* block_tables,
+                                           const int* context_lens, float scale, int num_seqs,
+                                           int num_heads, int num_kv_heads, int head_dim,
+                                           int block_size, int max_num_blocks_per_seq,
+                                           int num_blocks, hipStream_t stream) {
+    const Shape sh{num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_num_blocks_per_seq};
+    return decode_v1(output, query, key_cache, value_cache, block_tables, context_lens, scale, sh,
+                     num_blocks, stream, "swiftllm_hip_launch_paged_attention_v1");
+}
+
+void launch_paged_attention_v2(void* output, void* workspace, size_t workspace_bytes, void* query,
+                               void* key_cache, void* value_cache, int* block_tables,
+                               int* context_lens, float scale, int num_seqs, int num_heads,
+                               int num_kv_heads, int head_dim, int block_size,
+                               int max_num_blocks_per_seq, int partition_size, hipStream_t stream) {
+    const Shape sh{num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_num_blocks_per_seq};
+    decode_v2(output, workspace, workspace_bytes, query, key_cache, value_cache, block_tables,
+              context_lens, scale, sh, partition_size, 0, stream, "launch_paged_attention_v2");
+}
+
+int swiftllm_hip_launch_paged_attention_v2(void* output, void* workspace, size_t workspace_bytes,
+                                           const void* query, const void* key_cache,
+                                           const void* value_cache, const int* block_tables,
+                                           const int* context_lens, float scale, int num_seqs,
+                                           int num_heads, int num_kv_heads, int head_dim,
+                                           int block_size, int max_num_blocks_per_seq,
+                                           int partition_size, int num_blocks, hipStream_t stream) {
+    const Shape sh{num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_num_blocks_per_seq};
+    return decode_v2(output, workspace, workspace_bytes, query, key_cache, value_cache, block_tables,
+                     context_lens, scale, sh, partition_size, num_blocks, stream,
+                     "swiftllm_hip_launch_paged_attention_v2");
+}
+
+size_t swiftllm_hip_paged_attention_v2_workspace_size(int num_seqs, int num_heads, int num_kv_heads,
+                                                      int head_dim, int block_size,
+                                                      int max_num_blocks_per_seq,
+                                                      int partition_size) {
+    if (num_seqs < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 ||
+        head_dim <= 0 || block_size != kBlockTokens || max_num_blocks_per_seq < 0 ||
+        partition_size <= 0 || partition_size % kBlockTokens != 0) {
+        fail(SWIFTLLM_ERR_INVALID_PARAMETER, "swiftllm_hip_paged_attention_v2_workspace_size: bad shape");
+        return 0;
+    }
+    const Shape sh{num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_num_blocks_per_seq};
+    ok();
+    return v2_need(sh, partition_size).total;
+}
+
+int swiftllm_hip_workspace_clear(void* workspace, size_t bytes, hipStream_t stream) {
+    if (bytes == 0) return ok();
+    if (workspace == nullptr || !aligned(workspace, 4) || bytes % 4 != 0) {
+        return fail(SWIFTLLM_ERR_INVALID_PARAMETER,
+                    "swiftllm_hip_workspace_clear: null or misaligned workspace / size");
+    }
+    int rc = require_device();
+    if (rc != SWIFTLLM_OK) return rc;
+    ClearArgs a{static_cast<uint32_t*>(workspace), bytes / 4};
+    const size_t blocks = (a.words + 255) / 256;
+    const unsigned grid = static_cast<unsigned>(blocks < 4096 ? blocks : 4096);
+    return launched(launch(clear_kernel, dim3(grid), dim3(256), 0, stream, a),
+                    "swiftllm_hip_workspace_clear");
+}
+
+int swiftllm_hip_paged_attention_decode(void* output, const void* query, const void* key_cache,
+                                        const void* value_cache, const int32_t* block_tables,
+                                        const int32_t* context_lens,
+                                        const swiftllm_paged_attention_params* p,
+                                        hipStream_t stream) {
+    const char* who = "swiftllm_hip_paged_attention_decode";
+    if (p == nullptr) return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: null params", who);
+    const size_t lim = 0x7fffffff;
+    if (p->num_seqs > lim || p->num_heads > lim || p->num_kv_heads > lim || p->head_dim > lim ||
+        p->block_size > lim || p->max_context_len > lim || p->block_size == 0) {
+        return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: parameter out of range", who);
+    }
+    const size_t mb = (p->max_context_len + p->block_size - 1) / p->block_size;
+    const Shape sh{static_cast<int>(p->num_seqs), static_cast<int>(p->num_heads),
+                   static_cast<int>(p->num_kv_heads), static_cast<int>(p->head_dim),
+                   static_cast<int>(p->block_size), static_cast<int>(mb)};
+    return decode_v1(output, query, key_cache, value_cache, block_tables, context_lens, p->scale,
+                     sh, 0, stream, who);
+}
+
+int swiftllm_hip_gather_kv(const void* key_cache, const void* value_cache, const int* block_tables,
+                           const int* context_lens, int seq, int kv_head, int num_kv_heads,
+                           int head_dim, int block_size, int max_num_blocks_per_seq,
+                           int max_context_len, void* k_out, void* v_out, hipStream_t stream) {
+    const char* who = "swiftllm_hip_gather_kv";
+    if (seq < 0 || num_kv_heads <= 0 || kv_head < 0 || kv_head >= num_kv_heads || head_dim <= 0 ||
+        max_num_blocks_per_seq < 0 || max_context_len < 0) {
+        return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: bad shape", who);
+    }
+    if (block_size != kBlockTokens) {
+        return fail(SWIFTLLM_ERR_NOT_SUPPORTED, "%s: block_size %d (supported: 16)", who, block_size);
+    }
+    if (max_context_len > 0 &&
+        (!key_cache || !value_cache || !block_tables || !context_lens || !k_out || !v_out)) {
+        return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: null pointer", who);
+    }
+    int rc = require_device();
+    if (rc != SWIFTLLM_OK) return rc;
+    if (max_context_len == 0) return ok();
+    GatherArgs a{static_cast<const uint16_t*>(key_cache), static_cast<const uint16_t*>(value_cache),
+                 block_tables, context_lens, static_cast<uint16_t*>(k_out),
+                 static_cast<uint16_t*>(v_out), seq, kv_head, num_kv_heads, head_dim,
+                 max_num_blocks_per_seq, max_context_len};
+    const size_t n = static_cast<size_t>(max_context_len) * head_dim;
+    const size_t blocks = (n + 255) / 256;
+    const unsigned grid = static_cast<unsigned>(blocks < 65535 ? blocks : 65535);
+    return launched(launch(gather_kv_kernel, dim3(grid), dim3(256), 0, stream, a), who);
+}
+
+}  // extern "C"

@@ -1,0 +1,88 @@
+"""MoE top-k routing and expert-contiguous dispatch on the GPU.
+
+Mirrors the steps MoeMlp::forward names
+(crates/swiftllm-models/src/layers/mlp.rs:207-252: router logits, top-k,
+route tokens to experts, combine), which the reference leaves as a zero stub.
+Ranking conventions follow crates/swiftllm-core/src/sampling/mod.rs:366-385.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+
+from . import _lib
+from ._hip import DeviceArray, Stream
+from .paged_attention import check_status, workspace
+
+
+def moe_route(logits: DeviceArray, top_k: int, expert_ids: DeviceArray, weights: DeviceArray,
+              stream: Optional[Stream] = None) -> None:
+    """logits fp32 [T, E] -> expert_ids int32 [T, K], weights fp32 [T, K]."""
+    T, E = logits.shape
+    check_status(_lib.lib().swiftllm_hip_moe_route(
+        logits.ptr, T, E, top_k, expert_ids.ptr, weights.ptr,
+        stream.handle if stream else None))
+
+
+def moe_dispatch_workspace_size(num_tokens: int, num_experts: int, top_k: int) -> int:
+    n = _lib.lib().swiftllm_hip_moe_dispatch_workspace_size(num_tokens, num_experts, top_k)
+    if n == 0:
+        check_status(_lib.lib().swiftllm_hip_last_error() or -4)
+    return int(n)
+
+
+@dataclass
+class DispatchBuffers:
+    counts: DeviceArray        # int32 [E]
+    offsets: DeviceArray       # int32 [E + 1]
+    x_perm: Optional[DeviceArray]  # fp16 [T*K, hidden]
+    inverse: DeviceArray       # int32 [T, K]
+    sorted_token_ids: DeviceArray  # int32 [T*K]
+    workspace: DeviceArray
+
+    @classmethod
+    def allocate(cls, num_tokens: int, num_experts: int, top_k: int, hidden: int,
+                 with_rows: bool = True) -> "DispatchBuffers":
+        ws = workspace(moe_dispatch_workspace_size(num_tokens, num_experts, top_k))
+        return cls(
+            counts=DeviceArray((num_experts,), np.int32),
+            offsets=DeviceArray((num_experts + 1,), np.int32),
+            x_perm=DeviceArray((num_tokens * top_k, hidden), np.float16) if with_rows else None,
+            inverse=DeviceArray((num_tokens, top_k), np.int32),
+            sorted_token_ids=DeviceArray((max(num_tokens * top_k, 1),), np.int32),
+            workspace=ws,
+        )
+
+
+def moe_dispatch(expert_ids: DeviceArray, x: Optional[DeviceArray], num_experts: int,
+                 out: DispatchBuffers, stream: Optional[Stream] = None) -> None:
+    T, K = expert_ids.shape
+    hidden = x.shape[1] if x is not None else 0
+    check_status(_lib.lib().swiftllm_hip_moe_dispatch(
+        expert_ids.ptr, x.ptr if x is not None else None, T, K, num_experts, hidden,
+        out.counts.ptr, out.offsets.ptr, out.x_perm.ptr if out.x_perm is not None else None,
+        out.inverse.ptr, out.sorted_token_ids.ptr, out.workspace.ptr, out.workspace.nbytes,
+        stream.handle if stream else None))
+
+
+class MoeRouting:
+    """The routing half of MoeMlp (mlp.rs:209-221 fields num_experts,
+    num_experts_per_tok): route(logits) then dispatch(x)."""
+
+    def __init__(self, num_experts: int, num_experts_per_tok: int):
+        self.num_experts = num_experts
+        self.num_experts_per_tok = num_experts_per_tok
+
+    def forward(self, router_logits: DeviceArray, x: DeviceArray,
+                stream: Optional[Stream] = None):
+        T = router_logits.shape[0]
+        K = self.num_experts_per_tok
+        ids = DeviceArray((T, K), np.int32)
+        w = DeviceArray((T, K), np.float32)
+        moe_route(router_logits, K, ids, w, stream)
+        bufs = DispatchBuffers.allocate(T, self.num_experts, K, x.shape[1])
+        moe_dispatch(ids, x, self.num_experts, bufs, stream)
+        return ids, w, bufs

@@ -1,0 +1,257 @@
+"""Paged-attention decode on the GPU against the fp64 C oracle.
+
+Tolerance (fp16 in/out, fp32 accumulation): max abs error <= 2e-3 and max
+relative error <= 1e-2 with a 1e-3 floor on |ref| (tests/helpers.py).
+Index work (the block-table gather) is checked bit-exact.
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from helpers import DeviceWorkload, assert_attention_close
+from swiftllm_amd import paged_attention as pa
+from swiftllm_amd import workloads
+from swiftllm_amd._hip import DeviceArray, synchronize
+
+pytestmark = pytest.mark.gpu
+
+
+def _ref(w):
+    return oracle.decode_f64(w.q, w.key_cache, w.value_cache, w.block_tables, w.context_lens, w.scale)
+
+
+@pytest.mark.parametrize("variant,ps", [("v1", None), ("v2", 64), ("v2", 512), ("decode", None)])
+def test_config1_tiny_mha(dev, variant, ps):
+    w = workloads.decode_config(1, seed=11)
+    out = DeviceWorkload(w).run(variant, partition_size=ps)
+    assert_attention_close(out, _ref(w), f"config1 {variant} ps={ps}")
+
+
+@pytest.mark.parametrize("variant", ["v1", "v2"])
+def test_config2_llama3_8b(dev, variant):
+    w = workloads.decode_config(2, seed=2)
+    out = DeviceWorkload(w).run(variant)
+    assert_attention_close(out, _ref(w), f"config2 {variant}")
+
+
+def test_config3_long_context_split_k(dev):
+    # Llama-3-70B layer, 64 partitions of 512 tokens per sequence, one x8
+    # outlier key channel per kv head.
+    w = workloads.decode_config(3, seed=3)
+    dw = DeviceWorkload(w)
+    out = dw.run("v2", partition_size=512)
+    assert_attention_close(out, _ref(w), "config3 v2/512")
+    # split-K and single pass agree with each other as well as with the oracle
+    out1 = dw.run("v1")
+    assert_attention_close(out1, _ref(w), "config3 v1")
+
+
+def test_config4_ragged_step(dev):
+    """reshape_and_cache of the new tokens, then decode over the updated cache."""
+    w = workloads.decode_config(4, seed=4)
+    dw = DeviceWorkload(w)
+    sh = w.shape
+    k_new = DeviceArray.from_numpy(w.new_key)
+    v_new = DeviceArray.from_numpy(w.new_value)
+    sm = DeviceArray.from_numpy(w.slot_mapping)
+    pa.launch_reshape_and_cache(k_new, v_new, dw.kc, dw.vc, sm, sh["num_seqs"], sh["num_kv_heads"],
+                                sh["head_dim"], sh["block_size"], num_blocks=sh["num_blocks"])
+    synchronize()
+    kc_ref, vc_ref = w.key_cache.copy(), w.value_cache.copy()
+    oracle.reshape_and_cache(w.new_key, w.new_value, kc_ref, vc_ref, w.slot_mapping)
+    assert np.array_equal(dw.kc.numpy().view(np.uint16), kc_ref.view(np.uint16))
+    assert np.array_equal(dw.vc.numpy().view(np.uint16), vc_ref.view(np.uint16))
+    out = dw.run("v2", partition_size=512)
+    ref = oracle.decode_f64(w.q, kc_ref, vc_ref, w.block_tables, w.context_lens, w.scale)
+    assert_attention_close(out, ref, "config4 v2")
+
+
+@pytest.mark.parametrize("H,Hkv", [(8, 8), (16, 8), (32, 8), (64, 8), (16, 1), (32, 1), (48, 2)])
+@pytest.mark.parametrize("D", [64, 128])
+def test_gqa_groups(dev, H, Hkv, D):
+    """G = 1, 2, 4, 8, 16, 32 (two 16-head chunks) and 24 (a ragged chunk)."""
+    rng = np.random.default_rng(H * 1000 + Hkv * 10 + D)
+    S = 3
+    ctx = np.array([1, 37, 300], np.int32)
+    NB = 40
+    bt = np.zeros((S, 20), np.int32)
+    perm = rng.permutation(NB)
+    pos = 0
+    for s in range(S):
+        n = (ctx[s] + 15) // 16
+        bt[s, :n] = perm[pos:pos + n]
+        pos += n
+    kc = rng.standard_normal((NB, Hkv, D, 16)).astype(np.float16)
+    vc = rng.standard_normal((NB, Hkv, D, 16)).astype(np.float16)
+    q = rng.standard_normal((S, H, D)).astype(np.float16)
+    w = workloads.DecodeWorkload("gqa", q, kc, vc, bt, ctx, 1.0 / np.sqrt(D))
+    dw = DeviceWorkload(w)
+    ref = _ref(w)
+    for variant, ps in (("v1", None), ("v2", 32)):
+        assert_attention_close(dw.run(variant, partition_size=ps), ref, f"H{H} Hkv{Hkv} D{D} {variant}")
+
+
+def _poisoned(rng, S, ctx, D=128, H=32, Hkv=8, MB=None):
+    """Caches whose every slot outside the valid context holds NaN."""
+    need = (ctx + 15) // 16
+    NB = int(need.sum()) + 3
+    MB = MB or int(max(need.max(), 1))
+    bt = np.zeros((S, MB), np.int32)
+    perm = rng.permutation(NB)
+    pos = 0
+    kc = np.full((NB, Hkv, D, 16), np.nan, np.float16)
+    vc = np.full((NB, Hkv, D, 16), np.nan, np.float16)
+    for s in range(S):
+        n = need[s]
+        bt[s, :n] = perm[pos:pos + n]
+        pos += n
+        for j in range(n):
+            valid = min(16, ctx[s] - 16 * j)
+            kc[bt[s, j], :, :, :valid] = rng.standard_normal((Hkv, D, valid)).astype(np.float16)
+            vc[bt[s, j], :, :, :valid] = rng.standard_normal((Hkv, D, valid)).astype(np.float16)
+    q = rng.standard_normal((S, H, D)).astype(np.float16)
+    return workloads.DecodeWorkload("poison", q, kc, vc, bt, ctx.astype(np.int32), 1.0 / np.sqrt(D))
+
+
+@pytest.mark.parametrize("variant,ps", [("v1", None), ("v2", 16), ("v2", 48)])
+def test_edge_context_lengths(dev, variant, ps):
+    """ctx in {0, 1, 15, 16, 17, 31, 33, 200}; unused slots hold NaN."""
+    rng = np.random.default_rng(7)
+    ctx = np.array([0, 1, 15, 16, 17, 31, 33, 200], np.int32)
+    w = _poisoned(rng, len(ctx), ctx)
+    out = DeviceWorkload(w).run(variant, partition_size=ps)
+    ref = _ref(w)
+    assert np.all(out[0] == 0), "context 0 must give zeros"
+    # a single token: softmax weight 1, so the output is that token's V row exactly
+    v0 = w.value_cache[w.block_tables[1, 0], :, :, 0]            # [Hkv, D]
+    G = w.q.shape[1] // w.key_cache.shape[1]
+    assert np.array_equal(out[1].view(np.uint16), np.repeat(v0, G, axis=0).view(np.uint16))
+    assert_attention_close(out, ref, f"edge {variant} ps={ps}")
+
+
+def test_out_of_pool_blocks_skipped(dev):
+    """Block ids outside [0, num_blocks) contribute nothing; a sequence with
+    no valid block yields zeros. (Only with the bounded entry points.)"""
+    rng = np.random.default_rng(8)
+    w = workloads.decode_config(1, seed=8)
+    NB = w.key_cache.shape[0]
+    bt = w.block_tables.copy()
+    n0 = (w.context_lens[0] + 15) // 16
+    bt[0, :n0] = NB + 1000 + rng.integers(0, 5, n0)
+    w.block_tables = bt
+    for variant, ps in (("v1", None), ("v2", 32)):
+        out = DeviceWorkload(w).run(variant, partition_size=ps)
+        assert np.all(out[0] == 0)
+        ref = _ref(w)
+        assert_attention_close(out[1:], ref[1:], f"oob {variant}")
+
+
+def test_deterministic(dev):
+    w = workloads.decode_config(2, seed=5, num_seqs=8)
+    dw = DeviceWorkload(w)
+    a = dw.run("v2", partition_size=256).view(np.uint16)
+    b = dw.run("v2", partition_size=256).view(np.uint16)
+    assert np.array_equal(a, b)
+
+
+def test_workspace_reuse_across_shapes(dev):
+    """The split-K counters are left at zero after each call: the same
+    workspace serves calls of different shapes in a row."""
+    ws = pa.workspace(pa.paged_attention_v2_workspace_size(16, 32, 8, 128, 16, 256, 128))
+    for seed, S, ctx in ((1, 16, 4000), (2, 5, 700), (3, 16, 1500)):
+        w = workloads.decode_config(2, seed=seed, num_seqs=S, ctx=ctx)
+        dw = DeviceWorkload(w)
+        dw._ws = ws
+        assert_attention_close(dw.run("v2", partition_size=128), _ref(w), f"reuse S{S} ctx{ctx}")
+
+
+def test_gather_bit_exact(dev):
+    """The block-table gather (cu:80-87, 114-116) through the library's tile
+    addressing equals the numpy gather bit for bit."""
+    w = workloads.decode_config(1, seed=21)
+    dw = DeviceWorkload(w)
+    sh = w.shape
+    Lmax = int(w.context_lens.max()) + 5
+    D = sh["head_dim"]
+    for s in range(sh["num_seqs"]):
+        for kvh in (0, sh["num_kv_heads"] - 1):
+            ko = DeviceArray((Lmax, D), np.float16)
+            vo = DeviceArray((Lmax, D), np.float16)
+            pa.gather_kv(dw.kc, dw.vc, dw.bt, dw.ctx, s, kvh, sh["num_kv_heads"], D, 16,
+                         sh["max_num_blocks_per_seq"], Lmax, ko, vo)
+            synchronize()
+            L = int(w.context_lens[s])
+            kr = oracle.gather_kv(w.key_cache, w.block_tables[s], L)[kvh]
+            vr = oracle.gather_kv(w.value_cache, w.block_tables[s], L)[kvh]
+            kg, vg = ko.numpy(), vo.numpy()
+            assert np.array_equal(kg[:L].view(np.uint16), kr.view(np.uint16))
+            assert np.array_equal(vg[:L].view(np.uint16), vr.view(np.uint16))
+            assert np.all(kg[L:].view(np.uint16) == 0)
+
+
+def test_dropin_launchers(dev):
+    """The void launchers with the reference's argument lists."""
+    from swiftllm_amd import _lib
+
+    w = workloads.decode_config(1, seed=31)
+    dw = DeviceWorkload(w)
+    sh = w.shape
+    L = _lib.lib()
+    dw.out.fill_byte(0xFF)
+    L.launch_paged_attention_v1(dw.out.ptr, dw.q.ptr, dw.kc.ptr, dw.vc.ptr, dw.bt.ptr, dw.ctx.ptr,
+                                w.scale, sh["num_seqs"], sh["num_heads"], sh["num_kv_heads"],
+                                sh["head_dim"], sh["block_size"], sh["max_num_blocks_per_seq"], None)
+    synchronize()
+    assert L.swiftllm_hip_last_error() == 0
+    assert_attention_close(dw.out.numpy(), _ref(w), "launch_paged_attention_v1")
+    ws = pa.workspace(L.swiftllm_hip_paged_attention_v2_workspace_size(
+        sh["num_seqs"], sh["num_heads"], sh["num_kv_heads"], sh["head_dim"], 16,
+        sh["max_num_blocks_per_seq"], 64))
+    dw.out.fill_byte(0xFF)
+    L.launch_paged_attention_v2(dw.out.ptr, ws.ptr, ws.nbytes, dw.q.ptr, dw.kc.ptr, dw.vc.ptr, dw.bt.ptr,
+                                dw.ctx.ptr, w.scale, sh["num_seqs"], sh["num_heads"],
+                                sh["num_kv_heads"], sh["head_dim"], sh["block_size"],
+                                sh["max_num_blocks_per_seq"], 64, None)
+    synchronize()
+    assert L.swiftllm_hip_last_error() == 0
+    assert_attention_close(dw.out.numpy(), _ref(w), "launch_paged_attention_v2")
+    # an unsupported head_dim is refused without touching the output
+    L.launch_paged_attention_v1(dw.out.ptr, dw.q.ptr, dw.kc.ptr, dw.vc.ptr, dw.bt.ptr, dw.ctx.ptr,
+                                w.scale, sh["num_seqs"], sh["num_heads"], sh["num_kv_heads"], 96,
+                                sh["block_size"], sh["max_num_blocks_per_seq"], None)
+    assert L.swiftllm_hip_last_error() == pa.NotSupported.code
+
+
+def test_paged_attention_op(dev):
+    """PagedAttention.decode (paged_attention.rs:205-238): store the new K/V,
+    then attend, from host-side tables."""
+    rng = np.random.default_rng(41)
+    cfg = pa.PagedAttentionConfig.new(32, 8, 128, 16)
+    S, NB = 6, 64
+    ctx = np.array([1, 16, 17, 100, 250, 33])
+    perm = rng.permutation(NB)
+    tables, pos = [], 0
+    for L in ctx:
+        n = (L + 15) // 16
+        tables.append([int(b) for b in perm[pos:pos + n]])
+        pos += n
+    slots = [t[(L - 1) // 16] * 16 + (L - 1) % 16 for t, L in zip(tables, ctx)]
+    kc = rng.standard_normal((NB, 8, 128, 16)).astype(np.float16)
+    vc = rng.standard_normal((NB, 8, 128, 16)).astype(np.float16)
+    q = rng.standard_normal((S, 1, 32, 128)).astype(np.float16)
+    k = rng.standard_normal((S, 1, 8, 128)).astype(np.float16)
+    v = rng.standard_normal((S, 1, 8, 128)).astype(np.float16)
+    op = pa.PagedAttention(cfg, partition_size=32)
+    kc_d, vc_d = DeviceArray.from_numpy(kc), DeviceArray.from_numpy(vc)
+    out = op.decode(DeviceArray.from_numpy(q), DeviceArray.from_numpy(k), DeviceArray.from_numpy(v),
+                    kc_d, vc_d, tables, list(ctx), slots).numpy()
+    oracle.reshape_and_cache(k[:, 0], v[:, 0], kc, vc, np.array(slots, np.int32))
+    bt, ctx32 = pa.BatchedCacheMetadata(), None
+    for t, L in zip(tables, ctx):
+        bt.add_sequence(pa.SequenceCacheMetadata(int(L), t), [])
+    bt_arr, ctx32 = bt.pack(16)
+    ref = oracle.decode_f64(q[:, 0], kc, vc, bt_arr, ctx32, cfg.scale)
+    assert_attention_close(out[:, 0], ref, "PagedAttention.decode")
+    with pytest.raises(pa.InvalidParameter):
+        op.reshape_and_cache(DeviceArray.from_numpy(k), DeviceArray.from_numpy(v), kc_d, vc_d, slots[:-1])
