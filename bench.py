@@ -39,8 +39,12 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--variant", choices=["v1", "v2"], default="v2")
-    ap.add_argument("--partition", type=int, default=256)
+    ap.add_argument("--config", type=int, choices=[2, 3, 4], default=2,
+                    help="2: Llama-3-8B decode (the metric's workload); 3: long-context split-K; "
+                         "4: ragged step (cache write + decode)")
+    ap.add_argument("--variant", choices=["v1", "v2"], default=None,
+                    help="default: v1 for configs 2 and 4, v2 for config 3")
+    ap.add_argument("--partition", type=int, default=512)
     ap.add_argument("--rotate", type=int, default=4)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -64,8 +68,10 @@ def main():
         print("bench.py: no HIP device visible", file=sys.stderr)
         sys.exit(1)
 
+    if args.variant is None:
+        args.variant = "v2" if args.config == 3 else "v1"
     t0 = time.time()
-    w = workloads.decode_config(2, seed=args.seed)
+    w = workloads.decode_config(args.config, seed=args.seed)
     sh = w.shape
     kv_bytes = w.kv_bytes()
     alg_bytes = kv_bytes + w.other_bytes()
@@ -86,8 +92,17 @@ def main():
             sh["num_seqs"], sh["num_heads"], sh["num_kv_heads"], sh["head_dim"], sh["block_size"],
             sh["max_num_blocks_per_seq"], args.partition), stream)
 
+    if args.config == 4:
+        k_new = DeviceArray.from_numpy(w.new_key)
+        v_new = DeviceArray.from_numpy(w.new_value)
+        slots = DeviceArray.from_numpy(w.slot_mapping)
+
     def step(i):
         kc, vc = pools[i % len(pools)]
+        if args.config == 4:
+            pa.launch_reshape_and_cache(k_new, v_new, kc, vc, slots, sh["num_seqs"], sh["num_kv_heads"],
+                                        sh["head_dim"], sh["block_size"], num_blocks=sh["num_blocks"],
+                                        stream=stream)
         if args.variant == "v2":
             pa.paged_attention_v2(out, ws, q, kc, vc, bt, ctx, w.scale, sh["num_seqs"],
                                   sh["num_heads"], sh["num_kv_heads"], sh["head_dim"],
@@ -132,7 +147,7 @@ def main():
     achieved = alg_bytes / (ms * 1e-3) / 1e9      # all algorithmic bytes / kernel time
 
     traffic = None
-    tf = ROOT / "profiles" / "decode_config2_traffic.json"
+    tf = ROOT / "profiles" / f"decode_config{args.config}_traffic.json"
     if tf.exists():
         try:
             traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
@@ -154,11 +169,14 @@ def main():
         cpu_s = float(np.median(times))
         cpu = {"value": round(kv_bytes / cpu_s / 1e9, 3), "unit": "GB/s", "cores": int(threads),
                "kind": "port", "us_per_call": round(cpu_s * 1e6, 1),
-               "sample": f"full config-2 batch (same inputs), fp32 C restatement "
+               "sample": f"full config-{args.config} batch (same inputs, decode only), fp32 C restatement "
                          f"(oracle/oracle.c, OpenMP over (seq, kv head)), median of {len(times)} runs"}
         print(f"[bench] cpu baseline {cpu_s * 1e3:.1f} ms/call on {threads} threads", file=sys.stderr,
               flush=True)
 
+    workload_name = {2: "llama3-8b-decode-layer", 3: "llama3-70b-long-context-splitk",
+                     4: "ragged-continuous-batching-step"}[args.config]
+    ctx_desc = {2: "uniform[512,4096]", 3: "32768 (all)", 4: "lognormal(median 600, sigma 1) clip [1,8192]"}[args.config]
     rec = {
         "metric": "paged-attn decode KV-read GB/s (% HBM peak) + us/call @ Llama-3-8B shape",
         "value": round(value, 2),
@@ -174,14 +192,15 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16 in/out, f32 accumulate",
-        "data": "synthetic (seeded N(0,0.5) fp16, random permuted block tables)",
+        "data": "synthetic (seeded normal fp16 values, random permuted block tables)",
         "config": {
-            "workload": "llama3-8b-decode-layer",
+            "workload": workload_name,
             "num_seqs": sh["num_seqs"], "num_heads": sh["num_heads"],
             "num_kv_heads": sh["num_kv_heads"], "head_dim": sh["head_dim"],
-            "block_size": sh["block_size"], "context_lens": "uniform[512,4096]",
+            "block_size": sh["block_size"], "context_lens": ctx_desc,
             "sum_context": int(w.context_lens.sum()), "pool_blocks": sh["num_blocks"],
-            "kernel": f"paged_attention_{args.variant}" + (f"/partition{args.partition}" if args.variant == "v2" else ""),
+            "kernel": f"paged_attention_{args.variant}" + (f"/partition{args.partition}" if args.variant == "v2" else "")
+                      + ("+reshape_and_cache" if args.config == 4 else ""),
             "kv_pool_copies_rotated": len(pools), "seed": args.seed,
             "kv_bytes_per_call": kv_bytes, "algorithmic_bytes_per_call": alg_bytes,
         },
