@@ -26,6 +26,16 @@ int require_device();
 // Maps the result of hipLaunchKernel to a status.
 int launched(hipError_t err, const char* what);
 
+// Block tables and context lengths do not change during a kernel; reading
+// them through the constant address space lets the compiler use scalar loads
+// for wave-uniform indices even when the kernel stores to global memory in
+// the same loop (those stores would otherwise count as possible clobbers).
+typedef __attribute__((address_space(4))) const int const_int;
+
+__device__ __forceinline__ const const_int* as_const(const int* p) {
+    return (const const_int*)(p);
+}
+
 inline bool aligned(const void* p, size_t bytes) {
     return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
 }

@@ -105,16 +105,16 @@ __device__ __forceinline__ h4 load_kv(const f16* p) {
 }
 
 template <int D>
-__device__ __forceinline__ void load_tile(const DecodeArgs& a, int b, int kvh,
-                                          int loff, h4 (&k)[D / 16],
+__device__ __forceinline__ void load_tile(const f16* kc, const f16* vc, int Hkv, int num_blocks,
+                                          int b, int kvh, int loff, h4 (&k)[D / 16],
                                           h4 (&v)[D / 16]) {
     constexpr int NJ = D / 16;
     // An id outside the pool reads block 0 instead (in bounds); the caller
     // skips such a block.
-    const int bsafe = block_ok(b, a.num_blocks) ? b : 0;
-    const size_t base = kv_tile_offset(bsafe, kvh, a.Hkv, D) + loff;
-    const f16* kp = a.kc + base;
-    const f16* vp = a.vc + base;
+    const int bsafe = block_ok(b, num_blocks) ? b : 0;
+    const size_t base = kv_tile_offset(bsafe, kvh, Hkv, D) + loff;
+    const f16* kp = kc + base;
+    const f16* vp = vc + base;
 #pragma unroll
     for (int J = 0; J < NJ; ++J) {
         k[J] = load_kv(kp + kv_elem_offset(16 * J, 0));
@@ -124,6 +124,13 @@ __device__ __forceinline__ void load_tile(const DecodeArgs& a, int b, int kvh,
         v[J] = load_kv(vp + kv_elem_offset(16 * J, 0));
     }
 }
+
+// Q^T operand of step 2: lane (r, kg) holds q[h0 + r][16J + 4kg .. +3].
+template <int D>
+struct QOperand {
+    h4 v[D / 16];
+    __device__ __forceinline__ h4 get(int J) const { return v[J]; }
+};
 
 // Running softmax state of one wave: max (log2 domain), sum of
 // 2^15 * exp2(s - max) over this lane's token rows, and O^T accumulators.
@@ -139,7 +146,7 @@ struct WaveState {
 template <int D>
 __device__ __forceinline__ void attend_block(WaveState<D>& st, int nv, int kg,
                                              h4 (&kA)[D / 16], h4 (&vA)[D / 16],
-                                             const h4 (&qB)[D / 16], h4 ident,
+                                             const QOperand<D>& qB, h4 ident,
                                              float scale_log2) {
     constexpr int NJ = D / 16;
     if (nv < kBlockTokens) {
@@ -160,9 +167,9 @@ __device__ __forceinline__ void attend_block(WaveState<D>& st, int nv, int kg,
         const f4 t = mfma16(kA[J], ident, f4{0, 0, 0, 0});
         const h4 kT = to_h4(t);
         if (J & 1) {
-            s1 = mfma16(kT, qB[J], s1);
+            s1 = mfma16(kT, qB.get(J), s1);
         } else {
-            s0 = mfma16(kT, qB[J], s0);
+            s0 = mfma16(kT, qB.get(J), s0);
         }
     }
     // Step 3. Lane (r, kg) holds S^T[t = 4kg + i][g = r].
@@ -234,18 +241,8 @@ __device__ __forceinline__ int sequence_for_block(const int* ctx, int S, int r) 
     return s_seq;
 }
 
-// Waves per SIMD the register allocation must allow (0: compiler's choice).
-#ifndef SWIFTLLM_DECODE_WAVES_PER_EU
-#define SWIFTLLM_DECODE_WAVES_PER_EU 0
-#endif
-#if SWIFTLLM_DECODE_WAVES_PER_EU > 0
-#define SWIFTLLM_DECODE_OCCUPANCY __attribute__((amdgpu_waves_per_eu(SWIFTLLM_DECODE_WAVES_PER_EU)))
-#else
-#define SWIFTLLM_DECODE_OCCUPANCY
-#endif
-
 template <int D, int NW>
-__global__ __launch_bounds__(NW * 64) SWIFTLLM_DECODE_OCCUPANCY void paged_decode_kernel(const DecodeArgs a) {
+__global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeArgs a) {
     constexpr int NJ = D / 16;
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -285,14 +282,13 @@ __global__ __launch_bounds__(NW * 64) SWIFTLLM_DECODE_OCCUPANCY void paged_decod
     }
     if (part >= nparts) return;
 
-    // Q^T operand of step 2: lane (r, kg) holds q[h0 + r][16J + 4kg .. +3].
-    h4 qB[NJ];
+    QOperand<D> qB;
     {
         const f16* qp = a.q + (static_cast<size_t>(s) * a.H + h0 + min(r, gn - 1)) * D + 4 * kg;
 #pragma unroll
         for (int J = 0; J < NJ; ++J) {
             const h4 v = *reinterpret_cast<const h4*>(qp + 16 * J);
-            qB[J] = (r < gn) ? v : h4{0, 0, 0, 0};
+            qB.v[J] = (r < gn) ? v : h4{0, 0, 0, 0};
         }
     }
     // Identity operand of step 1: B[k = 4kg + i][n = r] = (k == n).
@@ -303,7 +299,7 @@ __global__ __launch_bounds__(NW * 64) SWIFTLLM_DECODE_OCCUPANCY void paged_decod
     }
     // Lane (r, kg) loads tile row 16J + r, tokens 4kg .. 4kg + 3.
     const int loff = kv_elem_offset(r, 4 * kg);
-    const int* btrow = a.bt + static_cast<size_t>(s) * a.MB;
+    const const_int* btrow = as_const(a.bt) + static_cast<size_t>(s) * a.MB;
 
     WaveState<D> st;
     st.m = -INFINITY;
@@ -312,32 +308,32 @@ __global__ __launch_bounds__(NW * 64) SWIFTLLM_DECODE_OCCUPANCY void paged_decod
     for (int J = 0; J < NJ; ++J) st.acc[J] = f4{0, 0, 0, 0};
 
     // Blocks jb0 + w, jb0 + w + NW, ... of this wave, double-buffered in
-    // registers: the next block's loads are in flight while one is computed.
+    // registers: the next block's loads are in flight while one is attended.
     // Two blocks per iteration with every load and every attend_block
     // unconditional, so all paths have the same loads in flight and the
     // compiler's wait counts stay exact. Past the wave's last block the
-    // prefetch reloads the current tile (a cache hit) and the odd tail is
-    // attended with nv = 0.
+    // prefetch reloads that block (a cache hit) and the odd tail is attended
+    // with nv = 0.
     const int first = jb0 + w;
     const int nbw = (jb1 > first) ? (jb1 - first + NW - 1) / NW : 0;
     if (nbw > 0) {
-        h4 kA[NJ], vA[NJ], kB[NJ], vB[NJ];
         const int last = first + (nbw - 1) * NW;
-        int bA = __builtin_amdgcn_readfirstlane(btrow[first]);
-        load_tile<D>(a, bA, kvh, loff, kA, vA);
+        auto block_at = [&](int j) { return __builtin_amdgcn_readfirstlane(btrow[min(j, last)]); };
+        auto valid_of = [&](int j, int b) {
+            return (j <= last && block_ok(b, a.num_blocks)) ? min(kBlockTokens, L - j * kBlockTokens) : 0;
+        };
+        h4 kA[NJ], vA[NJ], kB[NJ], vB[NJ];
+        int bA = block_at(first);
+        load_tile<D>(a.kc, a.vc, a.Hkv, a.num_blocks, bA, kvh, loff, kA, vA);
         for (int i = 0; i < nbw; i += 2) {
             const int jA = first + i * NW;
             const int jB = jA + NW;
-            const int jC = jB + NW;
-            const int bB = __builtin_amdgcn_readfirstlane(btrow[min(jB, last)]);
-            load_tile<D>(a, bB, kvh, loff, kB, vB);
-            attend_block<D>(st, block_ok(bA, a.num_blocks) ? min(kBlockTokens, L - jA * kBlockTokens) : 0,
-                            kg, kA, vA, qB, ident, a.scale_log2);
-            bA = __builtin_amdgcn_readfirstlane(btrow[min(jC, last)]);
-            load_tile<D>(a, bA, kvh, loff, kA, vA);
-            attend_block<D>(st,
-                            (jB <= last && block_ok(bB, a.num_blocks)) ? min(kBlockTokens, L - jB * kBlockTokens) : 0,
-                            kg, kB, vB, qB, ident, a.scale_log2);
+            const int bB = block_at(jB);
+            load_tile<D>(a.kc, a.vc, a.Hkv, a.num_blocks, bB, kvh, loff, kB, vB);
+            attend_block<D>(st, valid_of(jA, bA), kg, kA, vA, qB, ident, a.scale_log2);
+            bA = block_at(jB + NW);
+            load_tile<D>(a.kc, a.vc, a.Hkv, a.num_blocks, bA, kvh, loff, kA, vA);
+            attend_block<D>(st, valid_of(jB, bB), kg, kB, vB, qB, ident, a.scale_log2);
         }
     }
     float m_run = st.m;
@@ -394,6 +390,95 @@ __global__ __launch_bounds__(NW * 64) SWIFTLLM_DECODE_OCCUPANCY void paged_decod
     }
 }
 
+// Rescaled combine of P fragments (max m_p, sum l_p, normalised partial
+// o_p[d]) for gn <= 16 heads into out[g][d] = sum_p w_p o_p / sum_p w_p with
+// w_p = exp2(m_p - M) l_p. Fragment accessors: fm(p, g), fl(p, g) and
+// fo(p, g) (pointer to o_p of head g, 16-byte aligned). Runs on
+// kCombineThreads threads: the per-head max and denominator are reduced
+// across the workgroup, the weights go through LDS in chunks, and each
+// thread owns 4 consecutive outputs (one 16-byte load per fragment) of a
+// 1/F share of the fragments, F = threads / (gn * D / 4); an LDS pass adds
+// the F shares. The loads of a thread are independent, so many are in
+// flight at once.
+constexpr int kCombineThreads = 1024;
+constexpr int kCombineChunk = 256;
+
+template <int D, typename FM, typename FL, typename FO, typename OUT>
+__device__ __forceinline__ void combine_fragments(int P, int gn, FM fm, FL fl, FO fo, OUT out) {
+    constexpr int kWaves = kCombineThreads / 64;
+    __shared__ float s_red[16][kWaves];
+    __shared__ float s_M[16];
+    __shared__ float s_den[16];
+    __shared__ float s_w[16][kCombineChunk];
+    __shared__ f4 s_part[kCombineThreads];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wv = tid >> 6;
+    for (int g = 0; g < gn; ++g) {
+        float m = -INFINITY;
+        for (int p = tid; p < P; p += kCombineThreads) m = fmaxf(m, fm(p, g));
+        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        if (lane == 0) s_red[g][wv] = m;
+    }
+    __syncthreads();
+    if (tid < gn) {
+        float m = -INFINITY;
+        for (int i = 0; i < kWaves; ++i) m = fmaxf(m, s_red[tid][i]);
+        s_M[tid] = m;
+    }
+    __syncthreads();
+    for (int g = 0; g < gn; ++g) {
+        const float M = s_M[g];
+        float d = 0.0f;
+        for (int p = tid; p < P; p += kCombineThreads) {
+            const float mp = fm(p, g);
+            d += (mp == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mp - M) * fl(p, g);
+        }
+        for (int off = 32; off > 0; off >>= 1) d += __shfl_xor(d, off);
+        if (lane == 0) s_red[g][wv] = d;
+    }
+    __syncthreads();
+    if (tid < gn) {
+        float d = 0.0f;
+        for (int i = 0; i < kWaves; ++i) d += s_red[tid][i];
+        s_den[tid] = d;
+    }
+    const int quads = gn * (D / 4);
+    const int F = kCombineThreads / quads;  // fragment shares (>= 2)
+    const int quad = tid % quads;
+    const int share = tid / quads;
+    const int g = quad / (D / 4);
+    const int d4 = (quad - g * (D / 4)) * 4;
+    f4 acc = f4{0, 0, 0, 0};
+    for (int c0 = 0; c0 < P; c0 += kCombineChunk) {
+        const int cn = min(kCombineChunk, P - c0);
+        __syncthreads();
+        for (int i = tid; i < gn * cn; i += kCombineThreads) {
+            const int gg = i / cn;
+            const int p = c0 + (i - gg * cn);
+            const float mp = fm(p, gg);
+            s_w[gg][p - c0] = (mp == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mp - s_M[gg]) * fl(p, gg);
+        }
+        __syncthreads();
+        if (share < F) {
+#pragma unroll 8
+            for (int p = share; p < cn; p += F) {
+                acc += s_w[g][p] * *reinterpret_cast<const f4*>(fo(c0 + p, g) + d4);
+            }
+        }
+    }
+    s_part[tid] = acc;
+    __syncthreads();
+    if (tid < quads) {
+        f4 sum = s_part[tid];
+        for (int f = 1; f < F; ++f) sum += s_part[f * quads + tid];
+        const float den = s_den[g];
+        const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) out(g, d4 + i, sum[i] * inv);
+    }
+}
+
 // Split-K reduce: one workgroup per (sequence, kv head, head chunk) with more
 // than one partition; partition p contributes exp2(m_p - M) * l_p * o_p.
 struct ReduceArgs {
@@ -411,7 +496,7 @@ struct ReduceArgs {
 };
 
 template <int D>
-__global__ __launch_bounds__(256) void paged_reduce_kernel(const ReduceArgs a) {
+__global__ __launch_bounds__(kCombineThreads) void paged_reduce_kernel(const ReduceArgs a) {
     const int kvh = blockIdx.x / a.nhc;
     const int hc = blockIdx.x - kvh * a.nhc;
     const int s = blockIdx.y;
@@ -422,21 +507,360 @@ __global__ __launch_bounds__(256) void paged_reduce_kernel(const ReduceArgs a) {
     const int nblk = min((L + kBlockTokens - 1) / kBlockTokens, a.MB);
     const int nparts = (nblk + a.part_blocks - 1) / a.part_blocks;
     if (nparts <= 1) return;  // written directly by the partition kernel
-    for (int idx = threadIdx.x; idx < gn * D; idx += blockDim.x) {
-        const int g = idx / D;
-        const int d = idx - g * D;
-        const int h = h0 + g;
-        const size_t base = (static_cast<size_t>(s) * a.H + h) * a.MP;
-        float M = -INFINITY;
-        for (int p = 0; p < nparts; ++p) M = fmaxf(M, a.ws_max[base + p]);
-        float num = 0.0f, den = 0.0f;
-        for (int p = 0; p < nparts; ++p) {
-            const float mp = a.ws_max[base + p];
-            const float f = (mp == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mp - M) * a.ws_sum[base + p];
-            num += f * a.ws_out[(base + p) * D + d];
-            den += f;
+    const size_t hb = static_cast<size_t>(s) * a.H + h0;  // first head row of this chunk
+    combine_fragments<D>(
+        nparts, gn,
+        [&](int p, int g) { return a.ws_max[(hb + g) * a.MP + p]; },
+        [&](int p, int g) { return a.ws_sum[(hb + g) * a.MP + p]; },
+        [&](int p, int g) { return a.ws_out + ((hb + g) * a.MP + p) * D; },
+        [&](int g, int d, float v) { a.out[(hb + g) * D + d] = static_cast<f16>(v); });
+}
+
+// ---------------------------------------------------------------------------
+// Balanced ("stream-K") decode. The blocks of all sequences form one list,
+// sequence by sequence. A team of TS = Hkv * nhc consecutive waves (one per
+// kv head and head chunk) takes blocks [t*q, (t+1)*q) of that list, with
+// q = ceil(blocks / teams): every team gets the same number of blocks
+// whatever the context lengths, the grid runs in one round, and the waves of
+// a team read the kv-head tiles of the same blocks at the same time (one
+// block's tiles are contiguous in HBM). A wave walks its range as up to a few
+// segments (one per sequence it touches): a segment that covers the whole
+// sequence writes the final output; otherwise it leaves a fragment (max, sum,
+// partial output) in slot 2w (the wave's first segment) or 2w+1 (its last),
+// and paged_streamk_reduce_kernel combines the fragments of each split item.
+// ---------------------------------------------------------------------------
+constexpr int kStreamMaxSeqs = 4096;  // LDS prefix table bound
+constexpr int kFragHead = 32;         // floats before a fragment's partial output (16-byte aligned)
+constexpr int kStreamWaves = 4;       // waves per workgroup
+// Waves per SIMD the kernel's registers must allow: the grid is sized so
+// every wave is resident at once (4 SIMDs per CU).
+constexpr int kStreamWavesPerSimd = 3;
+
+struct StreamArgs {
+    f16* out;
+    const f16* q;
+    const f16* kc;
+    const f16* vc;
+    const int* bt;
+    const int* ctx;
+    float* frag;  // [2W][kFragHead + gstride * D]: max[16], sum[16], out[gstride][D]
+    // [W][4] + 1: first block of the sequence, sequence, blocks of the
+    // sequence (first segment of each wave, -1 if whole), then blocks per
+    // team. 64-bit on purpose: no store of the kernel has the block table's
+    // type.
+    long long* meta;
+    float scale_log2;
+    int S, H, Hkv, G, nhc, MB, num_blocks;
+    int W;  // waves in the grid
+};
+
+// Blocks per sequence -> exclusive prefix in s_pre[0..S] (s_pre[S] = total),
+// clamped context lengths in s_len. All threads of the workgroup take part.
+__device__ __forceinline__ void stream_prefix(const StreamArgs& a, int* s_pre, int* s_len,
+                                              int* s_tot) {
+    const int chunk = (a.S + blockDim.x - 1) / blockDim.x;
+    const int c0 = threadIdx.x * chunk;
+    int run = 0;
+    for (int c = c0; c < min(a.S, c0 + chunk); ++c) {
+        const int L0 = max(a.ctx[c], 0);
+        const int nb = min((L0 + kBlockTokens - 1) / kBlockTokens, a.MB);
+        s_len[c] = min(L0, nb * kBlockTokens);
+        s_pre[c] = run;  // local exclusive prefix, offset added below
+        run += nb;
+    }
+    s_tot[threadIdx.x] = run;
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        // exclusive scan of the (<= 256) chunk totals by wave 0
+        const int n = blockDim.x;
+        int v[4];
+        int sum = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int idx = threadIdx.x * 4 + i;
+            v[i] = idx < n ? s_tot[idx] : 0;
+            sum += v[i];
         }
-        a.out[(static_cast<size_t>(s) * a.H + h) * D + d] = static_cast<f16>(den > 0.0f ? num / den : 0.0f);
+        int incl = sum;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int t = __shfl_up(incl, off);
+            if (static_cast<int>(threadIdx.x) >= off) incl += t;
+        }
+        int ex = incl - sum;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int idx = threadIdx.x * 4 + i;
+            if (idx < n) s_tot[idx] = ex;
+            ex += v[i];
+        }
+        if (threadIdx.x == 63) s_pre[a.S] = incl;
+    }
+    __syncthreads();
+    const int off = s_tot[threadIdx.x];
+    for (int c = c0; c < min(a.S, c0 + chunk); ++c) s_pre[c] += off;
+    __syncthreads();
+}
+
+template <int D>
+__global__ __launch_bounds__(64 * kStreamWaves) __attribute__((amdgpu_waves_per_eu(kStreamWavesPerSimd)))
+void paged_decode_streamk_kernel(const StreamArgs a) {
+    constexpr int NJ = D / 16;
+    extern __shared__ int s_dyn[];
+    int* s_pre = s_dyn;              // [S + 1]
+    int* s_len = s_dyn + a.S + 1;    // [S]
+    __shared__ int s_tot[64 * kStreamWaves];
+    stream_prefix(a, s_pre, s_len, s_tot);
+
+    // Sequences without blocks are not in the list: zero their outputs here.
+    for (int sz = blockIdx.x; sz < a.S; sz += gridDim.x) {
+        if (s_pre[sz + 1] == s_pre[sz]) {
+            for (int i = threadIdx.x; i < a.H * D; i += blockDim.x) {
+                a.out[static_cast<size_t>(sz) * a.H * D + i] = static_cast<f16>(0.0f);
+            }
+        }
+    }
+
+    const int lane = threadIdx.x & 63;
+    const int w = blockIdx.x * kStreamWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15;
+    const int kg = lane >> 4;
+    const int gstride = min(16, a.G);
+    const int TS = a.Hkv * a.nhc;  // waves per team
+    const int teams = a.W / TS;
+    const int team = w / TS;
+    const int member = w - team * TS;
+    const int kvh = member / a.nhc;
+    const int hc = member - kvh * a.nhc;
+    const int g0 = hc * 16;
+    const int gn = min(16, a.G - g0);
+    const int h0 = kvh * a.G + g0;
+    const int U = __builtin_amdgcn_readfirstlane(s_pre[a.S]);
+    const int q = (U + teams - 1) / teams;
+    const int u0 = team < teams ? min(U, team * q) : U;
+    const int u1 = team < teams ? min(U, u0 + q) : U;
+    long long* meta = a.meta + 4 * w;
+    if (lane == 0) meta[0] = -1;  // no split first segment (overwritten below if there is one)
+    if (w == 0 && lane == 0) a.meta[4 * a.W] = q;  // blocks per team, for the reduce
+
+    h4 ident;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        ident[i] = (4 * kg + i == r) ? static_cast<f16>(1.0f) : static_cast<f16>(0.0f);
+    }
+    const int loff = kv_elem_offset(r, 4 * kg);
+
+    bool first_seg = true;
+    int u = u0;
+    while (u < u1) {
+        // sequence of block u: largest s with s_pre[s] <= u
+        int lo = 0, hi = a.S;
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (s_pre[mid] <= u) lo = mid; else hi = mid;
+        }
+        // Everything below is wave-uniform; readfirstlane keeps it in scalar
+        // registers so the block-table reads stay scalar loads.
+        const int s = __builtin_amdgcn_readfirstlane(lo);
+        const int L = __builtin_amdgcn_readfirstlane(s_len[s]);
+        const int pre = __builtin_amdgcn_readfirstlane(s_pre[s]);
+        const int nb = __builtin_amdgcn_readfirstlane(s_pre[s + 1]) - pre;
+        const int j0 = u - pre;
+        const int seg = min(nb - j0, u1 - u);
+
+        QOperand<D> qB;
+        {
+            const f16* qp = a.q + (static_cast<size_t>(s) * a.H + h0 + min(r, gn - 1)) * D + 4 * kg;
+#pragma unroll
+            for (int J = 0; J < NJ; ++J) {
+                const h4 v = *reinterpret_cast<const h4*>(qp + 16 * J);
+                qB.v[J] = (r < gn) ? v : h4{0, 0, 0, 0};
+            }
+        }
+        const const_int* btrow = as_const(a.bt) + static_cast<size_t>(s) * a.MB;
+        WaveState<D> st;
+        st.m = -INFINITY;
+        st.l = 0.0f;
+#pragma unroll
+        for (int J = 0; J < NJ; ++J) st.acc[J] = f4{0, 0, 0, 0};
+        {
+            const int last = j0 + seg - 1;
+            auto block_at = [&](int j) { return __builtin_amdgcn_readfirstlane(btrow[min(j, last)]); };
+            auto valid_of = [&](int j, int b) {
+                return (j <= last && block_ok(b, a.num_blocks)) ? min(kBlockTokens, L - j * kBlockTokens) : 0;
+            };
+            h4 kA[NJ], vA[NJ], kB[NJ], vB[NJ];
+            int bA = block_at(j0);
+            load_tile<D>(a.kc, a.vc, a.Hkv, a.num_blocks, bA, kvh, loff, kA, vA);
+            for (int i = 0; i < seg; i += 2) {
+                const int jA = j0 + i;
+                const int jB = jA + 1;
+                const int bB = block_at(jB);
+                load_tile<D>(a.kc, a.vc, a.Hkv, a.num_blocks, bB, kvh, loff, kB, vB);
+                attend_block<D>(st, valid_of(jA, bA), kg, kA, vA, qB, ident, a.scale_log2);
+                bA = block_at(jB + 1);
+                load_tile<D>(a.kc, a.vc, a.Hkv, a.num_blocks, bA, kvh, loff, kA, vA);
+                attend_block<D>(st, valid_of(jB, bB), kg, kB, vB, qB, ident, a.scale_log2);
+            }
+        }
+        float l_run = st.l;
+        l_run += __shfl_xor(l_run, 16);
+        l_run += __shfl_xor(l_run, 32);
+        const float inv = (l_run > 0.0f) ? 1.0f / l_run : 0.0f;
+        if (j0 == 0 && seg == nb) {
+            if (r < gn) {
+                f16* op = a.out + (static_cast<size_t>(s) * a.H + h0 + r) * D + 4 * kg;
+#pragma unroll
+                for (int J = 0; J < NJ; ++J) {
+                    h4 o;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) o[i] = static_cast<f16>(st.acc[J][i] * inv);
+                    *reinterpret_cast<h4*>(op + 16 * J) = o;
+                }
+            }
+        } else {
+            const int slot = 2 * w + (first_seg ? 0 : 1);
+            float* f = a.frag + static_cast<size_t>(slot) * (kFragHead + gstride * D);
+            if (r < gn) {
+                if (kg == 0) {
+                    f[r] = st.m;
+                    f[16 + r] = l_run;
+                }
+                float* fo = f + kFragHead + static_cast<size_t>(r) * D + 4 * kg;
+#pragma unroll
+                for (int J = 0; J < NJ; ++J) *reinterpret_cast<f4*>(fo + 16 * J) = st.acc[J] * inv;
+            }
+            if (first_seg && lane == 0) {
+                meta[0] = pre;  // first block of the sequence in the list
+                meta[1] = s;
+                meta[2] = nb;
+            }
+        }
+        first_seg = false;
+        u += seg;
+    }
+}
+
+// Combines the fragments of every split item, one wave per wave of the main
+// grid: wave w reduces the item of its first segment when that segment is
+// split, starts inside the sequence, and w's team is the first team to start
+// inside it (every other wave exits at once). Fragments of the item come from
+// the waves with the same team member index in teams ta..tb; there are few of
+// them (a sequence spans ceil(blocks / q) + 1 teams at most).
+struct StreamReduceArgs {
+    f16* out;
+    const float* frag;
+    const long long* meta;
+    int H, Hkv, G, nhc, W;
+    int gstride;
+};
+
+// Fragments per item the wave-level reduce keeps in LDS; items split over
+// more teams are combined in passes of this many fragments.
+constexpr int kReduceFragChunk = 64;
+
+template <int D>
+__global__ __launch_bounds__(256) void paged_streamk_reduce_kernel(const StreamReduceArgs a) {
+    __shared__ float s_w[4][16][kReduceFragChunk];  // per wave: weights w[g][i]
+    __shared__ float s_M[4][16];
+    __shared__ float s_den[4][16];
+    const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    const int w = blockIdx.x * 4 + wv;
+    if (w >= a.W) return;
+    const long long* m = a.meta + 4 * w;
+    if (m[0] < 0) return;
+    const int TS = a.Hkv * a.nhc;
+    const int q = static_cast<int>(a.meta[4 * a.W]);
+    const int ustart = static_cast<int>(m[0]);
+    const int team = w / TS;
+    const int ta = ustart / q;
+    if (team != ta + 1 || ustart == team * q) return;  // not the owner
+    const int member = w - team * TS;
+    const int s = static_cast<int>(m[1]);
+    const int nb = static_cast<int>(m[2]);
+    const int P = (ustart + nb - 1) / q - ta + 1;
+    const int kvh = member / a.nhc;
+    const int hc = member - kvh * a.nhc;
+    const int g0 = hc * 16;
+    const int gn = min(16, a.G - g0);
+    const int h0 = kvh * a.G + g0;
+    const size_t fs = kFragHead + static_cast<size_t>(a.gstride) * D;
+    // fragment i of the item comes from team ta + i
+    auto frag_of = [&](int i) {
+        const int t = ta + i;
+        const int v = t * TS + member;
+        const int slot = (t == ta && ta * q < ustart) ? 2 * v + 1 : 2 * v;
+        return a.frag + slot * fs;
+    };
+    // 1. per-head max over all fragments (one parallel batch of loads per pass)
+    if (lane < gn) s_M[wv][lane] = -INFINITY;
+    __builtin_amdgcn_wave_barrier();
+    for (int c0 = 0; c0 < P; c0 += kReduceFragChunk) {
+        const int cn = min(kReduceFragChunk, P - c0);
+        for (int k = lane; k < gn * cn; k += 64) {
+            const int g = k / cn;
+            s_w[wv][g][k - g * cn] = frag_of(c0 + k - g * cn)[g];
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (lane < gn) {
+            float mx = s_M[wv][lane];
+            for (int i = 0; i < cn; ++i) mx = fmaxf(mx, s_w[wv][lane][i]);
+            s_M[wv][lane] = mx;
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    if (lane < gn) s_den[wv][lane] = 0.0f;
+    const int quads = gn * (D / 4);
+    f4 acc[16 * D / 4 / 64];  // quads owned by this lane: lane, lane + 64, ...
+#pragma unroll
+    for (int k = 0; k < 16 * D / 4 / 64; ++k) acc[k] = f4{0, 0, 0, 0};
+    // 2. weights and weighted sums, kReduceFragChunk fragments per pass
+    for (int c0 = 0; c0 < P; c0 += kReduceFragChunk) {
+        const int cn = min(kReduceFragChunk, P - c0);
+        __builtin_amdgcn_wave_barrier();
+        for (int k = lane; k < gn * cn; k += 64) {
+            const int g = k / cn;
+            const float* f = frag_of(c0 + k - g * cn);
+            const float mp = f[g];
+            s_w[wv][g][k - g * cn] =
+                (mp == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mp - s_M[wv][g]) * f[16 + g];
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (lane < gn) {
+            float d = s_den[wv][lane];
+            for (int i = 0; i < cn; ++i) d += s_w[wv][lane][i];
+            s_den[wv][lane] = d;
+        }
+#pragma unroll
+        for (int k = 0; k < 16 * D / 4 / 64; ++k) {
+            const int qd = lane + 64 * k;
+            if (qd < quads) {
+                const int g = qd / (D / 4);
+                const int d4 = (qd - g * (D / 4)) * 4;
+#pragma unroll 8
+                for (int i = 0; i < cn; ++i) {
+                    acc[k] += s_w[wv][g][i] *
+                              *reinterpret_cast<const f4*>(frag_of(c0 + i) + kFragHead + static_cast<size_t>(g) * D + d4);
+                }
+            }
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+    f16* ob = a.out + (static_cast<size_t>(s) * a.H + h0) * D;
+#pragma unroll
+    for (int k = 0; k < 16 * D / 4 / 64; ++k) {
+        const int qd = lane + 64 * k;
+        if (qd < quads) {
+            const int g = qd / (D / 4);
+            const int d4 = (qd - g * (D / 4)) * 4;
+            const float den = s_den[wv][g];
+            const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+            h4 o;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = static_cast<f16>(acc[k][i] * inv);
+            *reinterpret_cast<h4*>(ob + static_cast<size_t>(g) * D + d4) = o;
+        }
     }
 }
 
@@ -533,6 +957,18 @@ int validate_decode(const char* who, const void* out, const void* q, const void*
     return SWIFTLLM_OK;
 }
 
+// Waves per workgroup of the single-pass kernel: the whole context of a
+// (sequence, kv head) is one workgroup, so it gets the most waves.
+#ifndef SWIFTLLM_WAVES_V1
+#define SWIFTLLM_WAVES_V1 8
+#endif
+constexpr int kWavesV1 = SWIFTLLM_WAVES_V1;
+// Waves per workgroup of a split-K partition.
+#ifndef SWIFTLLM_WAVES_V2
+#define SWIFTLLM_WAVES_V2 4
+#endif
+constexpr int kWavesV2 = SWIFTLLM_WAVES_V2;
+
 template <int D, int NW>
 hipError_t launch_decode_t(const DecodeArgs& a, int S, int mp_grid, hipStream_t stream) {
     const int gstride = a.G < 16 ? a.G : 16;
@@ -542,16 +978,10 @@ hipError_t launch_decode_t(const DecodeArgs& a, int S, int mp_grid, hipStream_t 
     return launch(paged_decode_kernel<D, NW>, grid, dim3(NW * 64), lds, stream, a);
 }
 
-hipError_t launch_decode(const DecodeArgs& a, int D, int NW, int S, int mp_grid,
-                         hipStream_t stream) {
-    if (D == 128) {
-        return NW == 16 ? launch_decode_t<128, 16>(a, S, mp_grid, stream)
-               : NW == 8 ? launch_decode_t<128, 8>(a, S, mp_grid, stream)
-                         : launch_decode_t<128, 4>(a, S, mp_grid, stream);
-    }
-    return NW == 16 ? launch_decode_t<64, 16>(a, S, mp_grid, stream)
-           : NW == 8 ? launch_decode_t<64, 8>(a, S, mp_grid, stream)
-                     : launch_decode_t<64, 4>(a, S, mp_grid, stream);
+template <int NW>
+hipError_t launch_decode(const DecodeArgs& a, int D, int S, int mp_grid, hipStream_t stream) {
+    return D == 128 ? launch_decode_t<128, NW>(a, S, mp_grid, stream)
+                    : launch_decode_t<64, NW>(a, S, mp_grid, stream);
 }
 
 DecodeArgs make_args(void* out, const void* q, const void* kc, const void* vc, const int* bt,
@@ -573,18 +1003,6 @@ DecodeArgs make_args(void* out, const void* q, const void* kc, const void* vc, c
     return a;
 }
 
-// Waves per workgroup of the single-pass kernel: the whole context of a
-// (sequence, kv head) is one workgroup, so it gets the most waves.
-#ifndef SWIFTLLM_WAVES_V1
-#define SWIFTLLM_WAVES_V1 8
-#endif
-constexpr int kWavesV1 = SWIFTLLM_WAVES_V1;
-// Waves per workgroup of a split-K partition.
-#ifndef SWIFTLLM_WAVES_V2
-#define SWIFTLLM_WAVES_V2 4
-#endif
-constexpr int kWavesV2 = SWIFTLLM_WAVES_V2;
-
 int decode_v1(void* out, const void* q, const void* kc, const void* vc, const int* bt,
               const int* ctx, float scale, const Shape& sh, int num_blocks, hipStream_t stream,
               const char* who) {
@@ -595,7 +1013,7 @@ int decode_v1(void* out, const void* q, const void* kc, const void* vc, const in
     DecodeArgs a = make_args(out, q, kc, vc, bt, ctx, scale, sh, num_blocks);
     a.part_blocks = 0;
     a.MP = 1;
-    return launched(launch_decode(a, sh.D, kWavesV1, sh.S, 1, stream), who);
+    return launched(launch_decode<kWavesV1>(a, sh.D, sh.S, 1, stream), who);
 }
 
 // Split-K workspace: max logits and exp sums [S][H][MP] and partial outputs
@@ -618,15 +1036,98 @@ V2Need v2_need(const Shape& sh, int partition_size) {
 
 template <int D>
 hipError_t launch_reduce_t(const ReduceArgs& r, int S, int Hkv, hipStream_t stream) {
-    return launch(paged_reduce_kernel<D>, dim3(Hkv * r.nhc, S), dim3(256), 0, stream, r);
+    return launch(paged_reduce_kernel<D>, dim3(Hkv * r.nhc, S), dim3(kCombineThreads), 0, stream, r);
 }
 
 int validate_partition(const char* who, int partition_size) {
-    if (partition_size <= 0 || partition_size % kBlockTokens != 0) {
+    if (partition_size < 0 || partition_size % kBlockTokens != 0) {
         return fail(SWIFTLLM_ERR_INVALID_PARAMETER,
-                    "%s: partition_size %d must be a positive multiple of 16", who, partition_size);
+                    "%s: partition_size %d must be 0 (balanced) or a positive multiple of 16", who,
+                    partition_size);
     }
     return SWIFTLLM_OK;
+}
+
+// Balanced mode: waves resident per CU (3 per SIMD at the kernel's register
+// count) times the device's CUs, so the whole grid runs in one round.
+constexpr int kStreamWavesPerCU = 4 * kStreamWavesPerSimd;
+constexpr int kDefaultCUs = 304;  // used to size workspaces when no device is visible
+
+int device_cus() {
+    static int cache[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return kDefaultCUs;
+    if (cache[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+            return kDefaultCUs;
+        }
+        cache[dev] = n;
+    }
+    return cache[dev];
+}
+
+struct StreamNeed {
+    int W;
+    size_t frag, total;
+};
+
+StreamNeed stream_need(const Shape& sh, int cus) {
+    StreamNeed n{};
+    n.W = cus * kStreamWavesPerCU;
+    const size_t gstride = static_cast<size_t>(std::min(16, sh.H / sh.Hkv));
+    n.frag = align_up(sizeof(float) * 2 * static_cast<size_t>(n.W) * (kFragHead + gstride * sh.D));
+    n.total = n.frag + align_up(sizeof(long long) * (4 * static_cast<size_t>(n.W) + 1));
+    return n;
+}
+
+int decode_balanced(void* out, void* ws, size_t ws_bytes, const void* q, const void* kc,
+                    const void* vc, const int* bt, const int* ctx, float scale, const Shape& sh,
+                    int num_blocks, hipStream_t stream, const char* who) {
+    const StreamNeed need = stream_need(sh, device_cus());
+    if (ws_bytes < need.total) {
+        return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: workspace of %zu bytes, %zu needed", who,
+                    ws_bytes, need.total);
+    }
+    DecodeArgs d = make_args(out, q, kc, vc, bt, ctx, scale, sh, num_blocks);
+    StreamArgs a{};
+    a.out = d.out;
+    a.q = d.q;
+    a.kc = d.kc;
+    a.vc = d.vc;
+    a.bt = bt;
+    a.ctx = ctx;
+    a.frag = reinterpret_cast<float*>(ws);
+    a.meta = reinterpret_cast<long long*>(static_cast<char*>(ws) + need.frag);
+    a.scale_log2 = d.scale_log2;
+    a.S = sh.S;
+    a.H = sh.H;
+    a.Hkv = sh.Hkv;
+    a.G = d.G;
+    a.nhc = d.nhc;
+    a.MB = sh.MB;
+    a.num_blocks = num_blocks;
+    a.W = need.W;
+    const size_t lds = sizeof(int) * (2 * static_cast<size_t>(sh.S) + 1);
+    const dim3 grid(need.W / kStreamWaves);
+    hipError_t err = sh.D == 128
+        ? launch(paged_decode_streamk_kernel<128>, grid, dim3(64 * kStreamWaves), lds, stream, a)
+        : launch(paged_decode_streamk_kernel<64>, grid, dim3(64 * kStreamWaves), lds, stream, a);
+    if (err != hipSuccess) return launched(err, who);
+    StreamReduceArgs r{};
+    r.out = a.out;
+    r.frag = a.frag;
+    r.meta = a.meta;
+    r.H = a.H;
+    r.Hkv = a.Hkv;
+    r.G = a.G;
+    r.nhc = a.nhc;
+    r.W = a.W;
+    r.gstride = std::min(16, a.G);
+    const dim3 rgrid((need.W + 3) / 4);
+    err = sh.D == 128 ? launch(paged_streamk_reduce_kernel<128>, rgrid, dim3(256), 0, stream, r)
+                      : launch(paged_streamk_reduce_kernel<64>, rgrid, dim3(256), 0, stream, r);
+    return launched(err, who);
 }
 
 int decode_v2(void* out, void* ws, size_t ws_bytes, const void* q, const void* kc, const void* vc,
@@ -635,6 +1136,21 @@ int decode_v2(void* out, void* ws, size_t ws_bytes, const void* q, const void* k
     int rc = validate_decode(who, out, q, kc, vc, bt, ctx, sh);
     if (rc != SWIFTLLM_OK) return rc;
     if ((rc = validate_partition(who, partition_size)) != SWIFTLLM_OK) return rc;
+    // Balanced mode needs its prefix table in LDS and at least 4 teams of
+    // Hkv * nhc waves; otherwise it falls back to partitions of 512 tokens.
+    if (partition_size == 0 &&
+        (sh.S > kStreamMaxSeqs ||
+         static_cast<long long>(sh.Hkv) * ((sh.H / sh.Hkv + 15) / 16) * 4 > device_cus() * kStreamWavesPerCU)) {
+        partition_size = 512;
+    }
+    if (partition_size == 0) {
+        if (sh.S > 0 && (ws == nullptr || !aligned(ws, 256))) {
+            return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: workspace null or not 256-byte aligned", who);
+        }
+        if ((rc = require_device()) != SWIFTLLM_OK) return rc;
+        if (sh.S == 0) return ok();
+        return decode_balanced(out, ws, ws_bytes, q, kc, vc, bt, ctx, scale, sh, num_blocks, stream, who);
+    }
     const V2Need need = v2_need(sh, partition_size);
     if (sh.S > 0) {
         if (ws == nullptr || !aligned(ws, 256)) {
@@ -654,7 +1170,7 @@ int decode_v2(void* out, void* ws, size_t ws_bytes, const void* q, const void* k
     a.ws_out = reinterpret_cast<float*>(base + 2 * need.stat);
     a.part_blocks = partition_size / kBlockTokens;
     a.MP = need.MP;
-    hipError_t err = launch_decode(a, sh.D, kWavesV2, sh.S, need.MP, stream);
+    hipError_t err = launch_decode<kWavesV2>(a, sh.D, sh.S, need.MP, stream);
     if (err != hipSuccess || need.MP <= 1) return launched(err, who);
     ReduceArgs r{};
     r.out = a.out;
@@ -729,12 +1245,18 @@ size_t swiftllm_hip_paged_attention_v2_workspace_size(int num_seqs, int num_head
                                                       int partition_size) {
     if (num_seqs < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 ||
         head_dim <= 0 || block_size != kBlockTokens || max_num_blocks_per_seq < 0 ||
-        partition_size <= 0 || partition_size % kBlockTokens != 0) {
+        partition_size < 0 || partition_size % kBlockTokens != 0) {
         fail(SWIFTLLM_ERR_INVALID_PARAMETER, "swiftllm_hip_paged_attention_v2_workspace_size: bad shape");
         return 0;
     }
     const Shape sh{num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_num_blocks_per_seq};
     ok();
+    if (partition_size == 0) {
+        int n = 0;
+        const int cus = (hipGetDeviceCount(&n) == hipSuccess && n > 0) ? device_cus() : kDefaultCUs;
+        // the balanced workspace also covers its partitioned fallback
+        return std::max(stream_need(sh, cus).total, v2_need(sh, 512).total);
+    }
     return v2_need(sh, partition_size).total;
 }
 

@@ -55,7 +55,7 @@ class DeviceWorkload:
                                   sh["num_seqs"], sh["num_heads"], sh["num_kv_heads"], sh["head_dim"],
                                   sh["block_size"], sh["max_num_blocks_per_seq"], num_blocks=nb)
         elif variant == "v2":
-            ps = partition_size or w.partition_size
+            ps = w.partition_size if partition_size is None else partition_size
             need = pa.paged_attention_v2_workspace_size(
                 sh["num_seqs"], sh["num_heads"], sh["num_kv_heads"], sh["head_dim"], sh["block_size"],
                 sh["max_num_blocks_per_seq"], ps)

@@ -21,18 +21,18 @@ def _ref(w):
     return oracle.decode_f64(w.q, w.key_cache, w.value_cache, w.block_tables, w.context_lens, w.scale)
 
 
-@pytest.mark.parametrize("variant,ps", [("v1", None), ("v2", 64), ("v2", 512), ("decode", None)])
+@pytest.mark.parametrize("variant,ps", [("v1", None), ("v2", 64), ("v2", 512), ("v2", 0), ("decode", None)])
 def test_config1_tiny_mha(dev, variant, ps):
     w = workloads.decode_config(1, seed=11)
     out = DeviceWorkload(w).run(variant, partition_size=ps)
     assert_attention_close(out, _ref(w), f"config1 {variant} ps={ps}")
 
 
-@pytest.mark.parametrize("variant", ["v1", "v2"])
-def test_config2_llama3_8b(dev, variant):
+@pytest.mark.parametrize("variant,ps", [("v1", None), ("v2", 512), ("v2", 0)])
+def test_config2_llama3_8b(dev, variant, ps):
     w = workloads.decode_config(2, seed=2)
-    out = DeviceWorkload(w).run(variant)
-    assert_attention_close(out, _ref(w), f"config2 {variant}")
+    out = DeviceWorkload(w).run(variant, partition_size=ps)
+    assert_attention_close(out, _ref(w), f"config2 {variant} ps={ps}")
 
 
 def test_config3_long_context_split_k(dev):
@@ -40,11 +40,12 @@ def test_config3_long_context_split_k(dev):
     # outlier key channel per kv head.
     w = workloads.decode_config(3, seed=3)
     dw = DeviceWorkload(w)
+    ref = _ref(w)
     out = dw.run("v2", partition_size=512)
-    assert_attention_close(out, _ref(w), "config3 v2/512")
-    # split-K and single pass agree with each other as well as with the oracle
-    out1 = dw.run("v1")
-    assert_attention_close(out1, _ref(w), "config3 v1")
+    assert_attention_close(out, ref, "config3 v2/512")
+    # single pass and balanced scheduling agree with the oracle as well
+    assert_attention_close(dw.run("v1"), ref, "config3 v1")
+    assert_attention_close(dw.run("v2", partition_size=0), ref, "config3 balanced")
 
 
 def test_config4_ragged_step(dev):
@@ -62,9 +63,9 @@ def test_config4_ragged_step(dev):
     oracle.reshape_and_cache(w.new_key, w.new_value, kc_ref, vc_ref, w.slot_mapping)
     assert np.array_equal(dw.kc.numpy().view(np.uint16), kc_ref.view(np.uint16))
     assert np.array_equal(dw.vc.numpy().view(np.uint16), vc_ref.view(np.uint16))
-    out = dw.run("v2", partition_size=512)
     ref = oracle.decode_f64(w.q, kc_ref, vc_ref, w.block_tables, w.context_lens, w.scale)
-    assert_attention_close(out, ref, "config4 v2")
+    for variant, ps in (("v2", 512), ("v2", 0), ("v1", None)):
+        assert_attention_close(dw.run(variant, partition_size=ps), ref, f"config4 {variant} ps={ps}")
 
 
 @pytest.mark.parametrize("H,Hkv", [(8, 8), (16, 8), (32, 8), (64, 8), (16, 1), (32, 1), (48, 2)])
@@ -88,8 +89,8 @@ def test_gqa_groups(dev, H, Hkv, D):
     w = workloads.DecodeWorkload("gqa", q, kc, vc, bt, ctx, 1.0 / np.sqrt(D))
     dw = DeviceWorkload(w)
     ref = _ref(w)
-    for variant, ps in (("v1", None), ("v2", 32)):
-        assert_attention_close(dw.run(variant, partition_size=ps), ref, f"H{H} Hkv{Hkv} D{D} {variant}")
+    for variant, ps in (("v1", None), ("v2", 32), ("v2", 0)):
+        assert_attention_close(dw.run(variant, partition_size=ps), ref, f"H{H} Hkv{Hkv} D{D} {variant} ps={ps}")
 
 
 def _poisoned(rng, S, ctx, D=128, H=32, Hkv=8, MB=None):
@@ -114,7 +115,7 @@ def _poisoned(rng, S, ctx, D=128, H=32, Hkv=8, MB=None):
     return workloads.DecodeWorkload("poison", q, kc, vc, bt, ctx.astype(np.int32), 1.0 / np.sqrt(D))
 
 
-@pytest.mark.parametrize("variant,ps", [("v1", None), ("v2", 16), ("v2", 48)])
+@pytest.mark.parametrize("variant,ps", [("v1", None), ("v2", 16), ("v2", 48), ("v2", 0)])
 def test_edge_context_lengths(dev, variant, ps):
     """ctx in {0, 1, 15, 16, 17, 31, 33, 200}; unused slots hold NaN."""
     rng = np.random.default_rng(7)
@@ -140,30 +141,32 @@ def test_out_of_pool_blocks_skipped(dev):
     n0 = (w.context_lens[0] + 15) // 16
     bt[0, :n0] = NB + 1000 + rng.integers(0, 5, n0)
     w.block_tables = bt
-    for variant, ps in (("v1", None), ("v2", 32)):
+    for variant, ps in (("v1", None), ("v2", 32), ("v2", 0)):
         out = DeviceWorkload(w).run(variant, partition_size=ps)
         assert np.all(out[0] == 0)
         ref = _ref(w)
         assert_attention_close(out[1:], ref[1:], f"oob {variant}")
 
 
-def test_deterministic(dev):
+@pytest.mark.parametrize("ps", [256, 0])
+def test_deterministic(dev, ps):
     w = workloads.decode_config(2, seed=5, num_seqs=8)
     dw = DeviceWorkload(w)
-    a = dw.run("v2", partition_size=256).view(np.uint16)
-    b = dw.run("v2", partition_size=256).view(np.uint16)
+    a = dw.run("v2", partition_size=ps).view(np.uint16)
+    b = dw.run("v2", partition_size=ps).view(np.uint16)
     assert np.array_equal(a, b)
 
 
-def test_workspace_reuse_across_shapes(dev):
-    """The split-K counters are left at zero after each call: the same
-    workspace serves calls of different shapes in a row."""
-    ws = pa.workspace(pa.paged_attention_v2_workspace_size(16, 32, 8, 128, 16, 256, 128))
+@pytest.mark.parametrize("ps", [128, 0])
+def test_workspace_reuse_across_shapes(dev, ps):
+    """The split-K workspace is plain scratch: one buffer serves calls of
+    different shapes in a row."""
+    ws = pa.workspace(pa.paged_attention_v2_workspace_size(16, 32, 8, 128, 16, 256, ps))
     for seed, S, ctx in ((1, 16, 4000), (2, 5, 700), (3, 16, 1500)):
         w = workloads.decode_config(2, seed=seed, num_seqs=S, ctx=ctx)
         dw = DeviceWorkload(w)
         dw._ws = ws
-        assert_attention_close(dw.run("v2", partition_size=128), _ref(w), f"reuse S{S} ctx{ctx}")
+        assert_attention_close(dw.run("v2", partition_size=ps), _ref(w), f"reuse S{S} ctx{ctx} ps={ps}")
 
 
 def test_gather_bit_exact(dev):
