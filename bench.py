@@ -39,16 +39,20 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", type=int, choices=[2, 3, 4], default=2,
+    ap.add_argument("--config", type=int, choices=[2, 3, 4, 5], default=2,
                     help="2: Llama-3-8B decode (the metric's workload); 3: long-context split-K; "
-                         "4: ragged step (cache write + decode)")
+                         "4: ragged step (cache write + decode); 5: MoE route + dispatch")
     ap.add_argument("--variant", choices=["v1", "v2"], default=None,
                     help="default: v1 for configs 2 and 4, v2 for config 3")
     ap.add_argument("--partition", type=int, default=512)
-    ap.add_argument("--rotate", type=int, default=4)
+    ap.add_argument("--rotate", type=int, default=None,
+                    help="input copies rotated between calls (default 4 for decode, 8 for MoE)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--samples", type=int, default=200, help="launches timed one by one for p10/p50/p90")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="before warmup, one device-to-device copy of this many MiB (a kernel of known "
+                         "traffic that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     return ap.parse_args()
 
 
@@ -68,6 +72,12 @@ def main():
         print("bench.py: no HIP device visible", file=sys.stderr)
         sys.exit(1)
 
+    if args.calib_copy_mib > 0:
+        calibrate(args.calib_copy_mib << 20)
+    if args.config == 5:
+        return bench_moe(args)
+    if args.rotate is None:
+        args.rotate = 4
     if args.variant is None:
         args.variant = "v2" if args.config == 3 else "v1"
     t0 = time.time()
@@ -146,13 +156,7 @@ def main():
     value = kv_bytes / (ms * 1e-3) / 1e9          # KV-read GB/s
     achieved = alg_bytes / (ms * 1e-3) / 1e9      # all algorithmic bytes / kernel time
 
-    traffic = None
-    tf = ROOT / "profiles" / f"decode_config{args.config}_traffic.json"
-    if tf.exists():
-        try:
-            traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
-        except Exception:
-            traffic = None
+    traffic = read_traffic(f"decode_config{args.config}_traffic.json")
 
     cpu = None
     if not args.no_cpu:
@@ -212,6 +216,123 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
         },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+def calibrate(nbytes):
+    """Kernels of known traffic for scaling rocprofv3's FETCH_SIZE and
+    WRITE_SIZE: one device-to-device copy of `nbytes` (reads and writes
+    `nbytes`) and one workspace clear of `nbytes` (writes `nbytes`)."""
+    from swiftllm_amd import _hip, _lib
+    from swiftllm_amd import paged_attention as pa
+    from swiftllm_amd._hip import DeviceArray
+
+    src, dst = DeviceArray((nbytes // 4,), np.uint32), DeviceArray((nbytes // 4,), np.uint32)
+    src.fill_byte(1)
+    _hip.synchronize()
+    _hip.check(_hip.hip().hipMemcpy(dst.ptr, src.ptr, nbytes, _hip.HIP_MEMCPY_D2D), "calibration copy")
+    pa.check_status(_lib.lib().swiftllm_hip_workspace_clear(dst.ptr, nbytes, None))
+    _hip.synchronize()
+    src.free()
+    dst.free()
+
+
+def read_traffic(name):
+    """HBM bytes per launch of the dominant kernel, from the committed
+    rocprofv3 counter summary, or None when there is none."""
+    tf = ROOT / "profiles" / name
+    if not tf.exists():
+        return None
+    try:
+        return json.loads(tf.read_text()).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def timed(step, stream, steps, warmup, samples):
+    """Warmup, then `steps` launches between two events on `stream`, then
+    `samples` individually timed launches. Returns (ms per step, p10, p50, p90 in us)."""
+    from swiftllm_amd import _hip
+    from swiftllm_amd._hip import Event
+
+    for i in range(warmup):
+        step(i)
+    stream.synchronize()
+    start, end = Event(), Event()
+    _hip.synchronize()
+    start.record(stream)
+    for i in range(steps):
+        step(i)
+    end.record(stream)
+    end.synchronize()
+    ms = start.elapsed_ms(end) / steps
+    evs = [(Event(), Event()) for _ in range(samples)]
+    for i, (a, b) in enumerate(evs):
+        a.record(stream)
+        step(i)
+        b.record(stream)
+    stream.synchronize()
+    per = np.array([a.elapsed_ms(b) * 1e3 for a, b in evs]) if evs else np.array([ms * 1e3])
+    return (ms,) + tuple(float(np.percentile(per, x)) for x in (10, 50, 90))
+
+
+def bench_moe(args):
+    """Config 5: Mixtral-8x7B-style routing + dispatch (4096 tokens, hidden 4096,
+    8 experts, top-2). Eight copies of the activations and outputs rotate so
+    the 256 MB Infinity Cache cannot hold a call's 100.9 MB."""
+    from swiftllm_amd import moe, workloads
+    from swiftllm_amd._hip import DeviceArray, Stream
+
+    wl = workloads.moe_config(seed=args.seed)
+    T, hidden = wl.x.shape
+    E, K = wl.num_experts, wl.top_k
+    stream = Stream()
+    copies = max(1, args.rotate or 8)
+    xs = [DeviceArray.from_numpy(wl.x) for _ in range(copies)]
+    logits = [DeviceArray.from_numpy(wl.logits) for _ in range(copies)]
+    bufs = [moe.DispatchBuffers.allocate(T, E, K, hidden) for _ in range(copies)]
+    ids = [DeviceArray((T, K), np.int32) for _ in range(copies)]
+    wts = [DeviceArray((T, K), np.float32) for _ in range(copies)]
+
+    def step(i):
+        c = i % copies
+        moe.moe_route(logits[c], K, ids[c], wts[c], stream)
+        moe.moe_dispatch(ids[c], xs[c], E, bufs[c], stream)
+
+    ms, p10, p50, p90 = timed(step, stream, args.steps, args.warmup, args.samples)
+    alg = wl.bytes()
+    value = alg / (ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+
+        t_budget, times = time.time(), []
+        while len(times) < 5 and time.time() - t_budget < 20.0:
+            t1 = time.perf_counter()
+            rids, _ = oracle.moe_route(wl.logits, K)
+            _, _, _, sorted_ids = oracle.moe_dispatch(rids, E)
+            _ = wl.x[sorted_ids]
+            times.append(time.perf_counter() - t1)
+        cpu_s = float(np.median(times))
+        cpu = {"value": round(alg / cpu_s / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+               "us_per_call": round(cpu_s * 1e6, 1),
+               "sample": "full config-5 batch: numpy/Python oracle route + stable counting sort + row gather"}
+    rec = {
+        "metric": "MoE top-2 route + dispatch GB/s (algorithmic bytes) + us/call @ Mixtral-8x7B shape",
+        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 6), "us_per_call": round(ms * 1e3, 3),
+        "us_per_call_p10_p50_p90": [round(p10, 2), round(p50, 2), round(p90, 2)],
+        "hbm_peak_frac": round(value / HBM_PEAK_GBS, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32 routing, f16 rows (bit copies)",
+        "data": "synthetic (seeded N(0,1) logits and activations)",
+        "config": {"workload": "mixtral-8x7b-moe-dispatch", "num_tokens": T, "hidden": hidden,
+                   "num_experts": E, "top_k": K, "copies_rotated": copies,
+                   "algorithmic_bytes_per_call": alg, "kernels": "moe_route + moe_rank + moe_permute"},
+        "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4),
+                     "traffic": read_traffic("moe_config5_traffic.json")},
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)

@@ -211,6 +211,50 @@ __device__ __forceinline__ void attend_block(WaveState<D>& st, int nv, int kg,
     }
 }
 
+// Attends `count` blocks of one sequence: logical blocks first,
+// first + stride, ... Blocks are double-buffered in registers, so the next
+// block's loads are in flight while one is attended. The steady-state loop
+// runs while at least three blocks are left: both of its loads are real
+// blocks, no load depends on a condition, and the compiler's wait counts stay
+// exact. The last one or two blocks are peeled off, so no tile is read twice.
+template <int D>
+__device__ __forceinline__ void attend_blocks(WaveState<D>& st, const const_int* btrow, int first,
+                                              int stride, int count, int L, const f16* kc,
+                                              const f16* vc, int Hkv, int num_blocks, int kvh,
+                                              int loff, int kg, const QOperand<D>& qB, h4 ident,
+                                              float scale_log2) {
+    constexpr int NJ = D / 16;
+    if (count <= 0) return;
+    auto block_at = [&](int j) { return __builtin_amdgcn_readfirstlane(btrow[j]); };
+    auto valid_of = [&](int j, int b) {
+        return block_ok(b, num_blocks) ? min(kBlockTokens, L - j * kBlockTokens) : 0;
+    };
+    h4 kA[NJ], vA[NJ], kB[NJ], vB[NJ];
+    int jA = first;
+    int bA = block_at(jA);
+    load_tile<D>(kc, vc, Hkv, num_blocks, bA, kvh, loff, kA, vA);
+    int left = count;
+    for (; left > 2; left -= 2) {
+        const int jB = jA + stride;
+        const int bB = block_at(jB);
+        load_tile<D>(kc, vc, Hkv, num_blocks, bB, kvh, loff, kB, vB);
+        attend_block<D>(st, valid_of(jA, bA), kg, kA, vA, qB, ident, scale_log2);
+        jA = jB + stride;
+        bA = block_at(jA);
+        load_tile<D>(kc, vc, Hkv, num_blocks, bA, kvh, loff, kA, vA);
+        attend_block<D>(st, valid_of(jB, bB), kg, kB, vB, qB, ident, scale_log2);
+    }
+    if (left == 2) {
+        const int jB = jA + stride;
+        const int bB = block_at(jB);
+        load_tile<D>(kc, vc, Hkv, num_blocks, bB, kvh, loff, kB, vB);
+        attend_block<D>(st, valid_of(jA, bA), kg, kA, vA, qB, ident, scale_log2);
+        attend_block<D>(st, valid_of(jB, bB), kg, kB, vB, qB, ident, scale_log2);
+    } else {
+        attend_block<D>(st, valid_of(jA, bA), kg, kA, vA, qB, ident, scale_log2);
+    }
+}
+
 // Longest-first dispatch: workgroups are issued roughly in blockIdx order, so
 // blockIdx.z = r serves the sequence with the r-th longest context (ties by
 // index). Long sequences start first and short ones fill in at the end.
@@ -307,35 +351,11 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeArgs 
 #pragma unroll
     for (int J = 0; J < NJ; ++J) st.acc[J] = f4{0, 0, 0, 0};
 
-    // Blocks jb0 + w, jb0 + w + NW, ... of this wave, double-buffered in
-    // registers: the next block's loads are in flight while one is attended.
-    // Two blocks per iteration with every load and every attend_block
-    // unconditional, so all paths have the same loads in flight and the
-    // compiler's wait counts stay exact. Past the wave's last block the
-    // prefetch reloads that block (a cache hit) and the odd tail is attended
-    // with nv = 0.
+    // Blocks jb0 + w, jb0 + w + NW, ... of this wave.
     const int first = jb0 + w;
     const int nbw = (jb1 > first) ? (jb1 - first + NW - 1) / NW : 0;
-    if (nbw > 0) {
-        const int last = first + (nbw - 1) * NW;
-        auto block_at = [&](int j) { return __builtin_amdgcn_readfirstlane(btrow[min(j, last)]); };
-        auto valid_of = [&](int j, int b) {
-            return (j <= last && block_ok(b, a.num_blocks)) ? min(kBlockTokens, L - j * kBlockTokens) : 0;
-        };
-        h4 kA[NJ], vA[NJ], kB[NJ], vB[NJ];
-        int bA = block_at(first);
-        load_tile<D>(a.kc, a.vc, a.Hkv, a.num_blocks, bA, kvh, loff, kA, vA);
-        for (int i = 0; i < nbw; i += 2) {
-            const int jA = first + i * NW;
-            const int jB = jA + NW;
-            const int bB = block_at(jB);
-            load_tile<D>(a.kc, a.vc, a.Hkv, a.num_blocks, bB, kvh, loff, kB, vB);
-            attend_block<D>(st, valid_of(jA, bA), kg, kA, vA, qB, ident, a.scale_log2);
-            bA = block_at(jB + NW);
-            load_tile<D>(a.kc, a.vc, a.Hkv, a.num_blocks, bA, kvh, loff, kA, vA);
-            attend_block<D>(st, valid_of(jB, bB), kg, kB, vB, qB, ident, a.scale_log2);
-        }
-    }
+    attend_blocks<D>(st, btrow, first, NW, nbw, L, a.kc, a.vc, a.Hkv, a.num_blocks, kvh, loff, kg,
+                     qB, ident, a.scale_log2);
     float m_run = st.m;
     float l_run = st.l;
     f4 (&acc)[NJ] = st.acc;
@@ -683,26 +703,8 @@ void paged_decode_streamk_kernel(const StreamArgs a) {
         st.l = 0.0f;
 #pragma unroll
         for (int J = 0; J < NJ; ++J) st.acc[J] = f4{0, 0, 0, 0};
-        {
-            const int last = j0 + seg - 1;
-            auto block_at = [&](int j) { return __builtin_amdgcn_readfirstlane(btrow[min(j, last)]); };
-            auto valid_of = [&](int j, int b) {
-                return (j <= last && block_ok(b, a.num_blocks)) ? min(kBlockTokens, L - j * kBlockTokens) : 0;
-            };
-            h4 kA[NJ], vA[NJ], kB[NJ], vB[NJ];
-            int bA = block_at(j0);
-            load_tile<D>(a.kc, a.vc, a.Hkv, a.num_blocks, bA, kvh, loff, kA, vA);
-            for (int i = 0; i < seg; i += 2) {
-                const int jA = j0 + i;
-                const int jB = jA + 1;
-                const int bB = block_at(jB);
-                load_tile<D>(a.kc, a.vc, a.Hkv, a.num_blocks, bB, kvh, loff, kB, vB);
-                attend_block<D>(st, valid_of(jA, bA), kg, kA, vA, qB, ident, a.scale_log2);
-                bA = block_at(jB + 1);
-                load_tile<D>(a.kc, a.vc, a.Hkv, a.num_blocks, bA, kvh, loff, kA, vA);
-                attend_block<D>(st, valid_of(jB, bB), kg, kB, vB, qB, ident, a.scale_log2);
-            }
-        }
+        attend_blocks<D>(st, btrow, j0, 1, seg, L, a.kc, a.vc, a.Hkv, a.num_blocks, kvh, loff, kg,
+                         qB, ident, a.scale_log2);
         float l_run = st.l;
         l_run += __shfl_xor(l_run, 16);
         l_run += __shfl_xor(l_run, 32);
