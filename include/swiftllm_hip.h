@@ -122,8 +122,8 @@ size_t swiftllm_hip_paged_attention_v2_workspace_size(
     int block_size, int max_num_blocks_per_seq, int partition_size);
 
 /* Zero-fills `bytes` bytes at `workspace` with a kernel (no memset node, so
- * it may be captured in a graph). Workspaces that must start at zero (MoE
- * dispatch) are cleared with it once after allocation. */
+ * it may be captured in a graph). No workspace of this library needs it; it
+ * is there for callers that want deterministic scratch contents. */
 int swiftllm_hip_workspace_clear(void* workspace, size_t bytes,
                                  hipStream_t stream);
 
@@ -219,9 +219,10 @@ size_t swiftllm_hip_moe_dispatch_workspace_size(int num_tokens,
  *   x_perm[row(t,k), :]   = x[t, :]          (fp16 bit copy, hidden wide)
  *   inverse[t, k]         = row(t,k)
  *   sorted_token_ids[row] = t
- * `workspace` (swiftllm_hip_moe_dispatch_workspace_size bytes) must be
- * zero-filled once after allocation; each call leaves it ready again.
- * x_perm may be NULL to compute the index arrays only. */
+ * `workspace` (swiftllm_hip_moe_dispatch_workspace_size bytes, 256-byte
+ * aligned) is plain scratch: no initialisation. Ids outside [0, E) are
+ * dropped (inverse = -1). x_perm may be NULL to compute the index arrays
+ * only. */
 int swiftllm_hip_moe_dispatch(const int32_t* expert_ids, const void* x,
                               int num_tokens, int top_k, int num_experts,
                               int hidden, int32_t* expert_counts,
@@ -229,6 +230,19 @@ int swiftllm_hip_moe_dispatch(const int32_t* expert_ids, const void* x,
                               int32_t* inverse, int32_t* sorted_token_ids,
                               void* workspace, size_t workspace_bytes,
                               hipStream_t stream);
+
+/* swiftllm_hip_moe_route followed by swiftllm_hip_moe_dispatch, with the
+ * routing done inside the dispatch's ranking kernel (one launch fewer, and
+ * the ids are not re-read). Same outputs as the two calls; the same
+ * workspace size. */
+int swiftllm_hip_moe_route_dispatch(const float* logits, const void* x,
+                                    int num_tokens, int top_k, int num_experts,
+                                    int hidden, int32_t* expert_ids,
+                                    float* weights, int32_t* expert_counts,
+                                    int32_t* expert_offsets, void* x_perm,
+                                    int32_t* inverse, int32_t* sorted_token_ids,
+                                    void* workspace, size_t workspace_bytes,
+                                    hipStream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* 5. Block-table gather check: materialise the K and V of (seq, kv_head) as */

@@ -11,13 +11,27 @@
 //           descending, ties to the lower index), then weights
 //           w_k = exp(x_k - x_max) / sum_k' exp(x_k' - x_max), which equals the
 //           softmax probabilities renormalised over the selected experts. The
-//           few exponentials per token run in fp64.
-// dispatch: (1) one wave per 64 tokens ranks its entries among equal experts
-//           with ballots (stable (t, k) order) and counts them; the last
-//           workgroup to finish scans the chunk counts into per-(chunk,
-//           expert) row bases. (2) one wave per token writes the inverse index
-//           and sorted token ids and copies the token's row once from HBM
-//           into its K destination rows with 16-byte accesses.
+//           few exponentials per token run in fp64. Rows of up to 16 logits
+//           are loaded into registers at once.
+// dispatch: two kernels, with no grid-wide synchronisation inside either.
+//           (1) rank: one wave per 64-token chunk ranks the chunk's entries
+//               among equal experts with ballots (stable (t, k) order) and
+//               stores per-(chunk, expert) counts. The fused entry point routes
+//               the chunk's tokens first, in the same wave.
+//           (2) permute: each workgroup scans the chunk counts (up to 4096
+//               of them) in LDS into per-(chunk, expert) prefixes and expert
+//               offsets, while the first loads of its rows are in flight.
+//               Then one wave per token computes the K destination rows,
+//               writes the inverse index and sorted token ids, and copies the
+//               token's row once from HBM into its K destinations, every load
+//               of a batch issued before its stores. The destination rows are
+//               written with nontemporal stores (measured faster than plain
+//               ones for this one-read, K-write pattern).
+//           Larger count matrices get a scan kernel between the two: one
+//           workgroup per expert turns its column into exclusive prefixes
+//           and the expert's total.
+//           Kernel boundaries order the phases, so the workspace needs no
+//           initialisation and no device-scope fences are issued.
 
 #include <climits>
 #include <cmath>
@@ -39,32 +53,26 @@ struct RouteArgs {
     int E;
 };
 
+constexpr int kRouteRegs = 16;  // rows up to this many experts are held in registers
+
+// One argmax pass of the top-K selection: the largest logit among experts
+// not yet taken; the strict '>' keeps the lowest index among equal logits.
 template <int K>
-__global__ __launch_bounds__(256) void moe_route_kernel(const RouteArgs a) {
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= a.T) return;
-    const float* row = a.logits + static_cast<size_t>(t) * a.E;
-    // K argmax passes over the row, each skipping the experts already taken;
-    // the strict '>' keeps the lowest index among equal logits.
-    float bv[K];
-    int bi[K];
+__device__ __forceinline__ void consider(int e, float x, int k, const int (&bi)[K], float& best,
+                                         int& besti) {
+    bool taken = false;
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
-        float best = 0.0f;
-        int besti = -1;
-        for (int e = 0; e < a.E; ++e) {
-            bool taken = false;
-#pragma unroll
-            for (int j = 0; j < k; ++j) taken = taken || (bi[j] == e);
-            const float x = row[e];
-            if (!taken && (besti < 0 || x > best)) {
-                best = x;
-                besti = e;
-            }
-        }
-        bv[k] = best;
-        bi[k] = besti;
+    for (int j = 0; j < K; ++j) taken = taken || (j < k && bi[j] == e);
+    if (!taken && (besti < 0 || x > best)) {
+        best = x;
+        besti = e;
     }
+}
+
+// Writes ids and weights w_k = exp(x_k - x_0) / sum_k' exp(x_k' - x_0) of token t.
+template <int K>
+__device__ __forceinline__ void write_route(const RouteArgs& a, int t, const float (&bv)[K],
+                                            const int (&bi)[K]) {
     double ex[K];
     double sum = 0.0;
 #pragma unroll
@@ -79,42 +87,66 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const RouteArgs a) {
     }
 }
 
-struct RankArgs {
-    const int* ids;
-    int* rank;       // [T*K] rank among equal experts inside the 64-token chunk
-    int* chunk;      // [nchunks][E] counts; rewritten as row bases by the scan
-    int* counts;     // [E]
-    int* offsets;    // [E + 1]
-    unsigned* ticket;
-    int T;
-    int E;
-    int nchunks;
-};
+// Top-K of one row of logits into bv (values) and bi (expert ids).
+template <int K>
+__device__ __forceinline__ void select_topk(const float* row, int E, float (&bv)[K], int (&bi)[K]) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) bi[k] = -1;
+    if (E <= kRouteRegs) {
+        // All loads issued together; the K passes then run on registers.
+        float v[kRouteRegs];
+#pragma unroll
+        for (int e = 0; e < kRouteRegs; ++e) v[e] = (e < E) ? row[e] : 0.0f;
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            float best = 0.0f;
+            int besti = -1;
+#pragma unroll
+            for (int e = 0; e < kRouteRegs; ++e) {
+                if (e < E) consider<K>(e, v[e], k, bi, best, besti);
+            }
+            bv[k] = best;
+            bi[k] = besti;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            float best = 0.0f;
+            int besti = -1;
+            for (int e = 0; e < E; ++e) consider<K>(e, row[e], k, bi, best, besti);
+            bv[k] = best;
+            bi[k] = besti;
+        }
+    }
+}
 
 template <int K>
-__global__ __launch_bounds__(256) void moe_rank_kernel(const RankArgs a) {
-    __shared__ int s_cnt[4][kMaxExperts];
-    __shared__ int s_tot[kMaxExperts + 1];
-    __shared__ int s_last;
-    const int lane = threadIdx.x & 63;
-    const int wv = threadIdx.x >> 6;
-    const int c = blockIdx.x * 4 + wv;  // chunk of this wave
-    for (int e = lane; e < a.E; e += 64) s_cnt[wv][e] = 0;
+__global__ __launch_bounds__(256) void moe_route_kernel(const RouteArgs a) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= a.T) return;
+    float bv[K];
+    int bi[K];
+    select_topk<K>(a.logits + static_cast<size_t>(t) * a.E, a.E, bv, bi);
+    write_route<K>(a, t, bv, bi);
+}
 
-    const int t = c * kChunkTokens + lane;
-    const bool live = (c < a.nchunks) && (t < a.T);
-    int id[K];
+// Ranks the entries of one 64-token chunk among equal experts, stable in
+// (t, k) order: rk[k] = number of earlier entries of the chunk with the same
+// expert, or -1 for an id outside [0, E). Lane 0 stores the count of every
+// expert present in the chunk to cnt[e]; entries of absent experts are left
+// as they are. One round per distinct expert: the lowest pending entry of
+// the wave names the expert, and ballots over the K slots give each entry
+// the number of equal entries below it.
+template <int K>
+__device__ __forceinline__ void rank_chunk(const int (&id)[K], int (&rk)[K], int E, int lane,
+                                           int* cnt) {
     bool pend[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-        id[k] = live ? a.ids[static_cast<size_t>(t) * K + k] : -1;
-        pend[k] = live && id[k] >= 0 && id[k] < a.E;
+        pend[k] = id[k] >= 0 && id[k] < E;
+        rk[k] = -1;
     }
     const unsigned long long below_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    int rk[K];
-#pragma unroll
-    for (int k = 0; k < K; ++k) rk[k] = -1;
-    // Peel one expert at a time: as many rounds as distinct experts in the chunk.
     while (true) {
         int cand = -1;
 #pragma unroll
@@ -123,7 +155,7 @@ __global__ __launch_bounds__(256) void moe_rank_kernel(const RankArgs a) {
         }
         const unsigned long long any = __ballot(cand >= 0);
         if (any == 0ull) break;
-        const int e = __shfl(cand, __ffsll(static_cast<long long>(any)) - 1);
+        const int e = __builtin_amdgcn_readlane(cand, __ffsll(static_cast<long long>(any)) - 1);
         int below = 0, total = 0;
 #pragma unroll
         for (int k = 0; k < K; ++k) {
@@ -140,112 +172,255 @@ __global__ __launch_bounds__(256) void moe_rank_kernel(const RankArgs a) {
                 pend[k] = false;
             }
         }
-        if (lane == 0) s_cnt[wv][e] = total;
+        if (lane == 0) cnt[e] = total;
     }
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d);
+        if (lane >= d) x += y;
+    }
+    return x;
+}
+
+// ---------------------------------------------------------------------------
+// (1) Rank, optionally after routing.
+// ---------------------------------------------------------------------------
+struct RankArgs {
+    const float* logits;  // non-null: route the chunk first (ids and w are outputs)
+    int* ids;             // [T*K]
+    float* w;             // [T*K], with logits
+    int* rank;            // [T*K] rank among equal experts inside the 64-token chunk
+    int* cnt;             // [nchunks][E] counts
+    int T;
+    int E;
+    int nchunks;
+};
+
+constexpr int kRankWaves = 4;
+
+template <int K>
+__global__ __launch_bounds__(64 * kRankWaves) void moe_rank_kernel(const RankArgs a) {
+    __shared__ int s_cnt[kRankWaves][kMaxExperts];
+    const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    const int c = blockIdx.x * kRankWaves + wv;  // chunk of this wave
+    if (c >= a.nchunks) return;                   // whole waves only; no barriers below
+    for (int e = lane; e < a.E; e += 64) s_cnt[wv][e] = 0;
+
+    const int t = c * kChunkTokens + lane;
+    const bool live = t < a.T;
+    int id[K], rk[K];
+    if (a.logits != nullptr) {
+        float bv[K];
+        if (live) {
+            select_topk<K>(a.logits + static_cast<size_t>(t) * a.E, a.E, bv, id);
+            RouteArgs ra{a.logits, a.ids, a.w, a.T, a.E};
+            write_route<K>(ra, t, bv, id);
+        } else {
+#pragma unroll
+            for (int k = 0; k < K; ++k) id[k] = -1;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < K; ++k) id[k] = live ? a.ids[static_cast<size_t>(t) * K + k] : -1;
+    }
+    rank_chunk<K>(id, rk, a.E, lane, s_cnt[wv]);
     if (live) {
 #pragma unroll
         for (int k = 0; k < K; ++k) a.rank[static_cast<size_t>(t) * K + k] = rk[k];
     }
-    __syncthreads();
-    if (c < a.nchunks) {
-        for (int e = lane; e < a.E; e += 64) a.chunk[static_cast<size_t>(c) * a.E + e] = s_cnt[wv][e];
-    }
-
-    // The last workgroup to arrive scans the chunk counts.
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const unsigned prev = atomicAdd(a.ticket, 1u);
-        const int last = (prev == gridDim.x - 1);
-        if (last) *a.ticket = 0u;
-        s_last = last;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    for (int e = threadIdx.x; e < a.E; e += blockDim.x) {
-        int run = 0;
-        for (int cc = 0; cc < a.nchunks; ++cc) run += a.chunk[static_cast<size_t>(cc) * a.E + e];
-        s_tot[e] = run;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int run = 0;
-        for (int e = 0; e < a.E; ++e) {
-            const int n = s_tot[e];
-            s_tot[e] = run;
-            a.offsets[e] = run;
-            a.counts[e] = n;
-            run += n;
-        }
-        a.offsets[a.E] = run;
-    }
-    __syncthreads();
-    for (int e = threadIdx.x; e < a.E; e += blockDim.x) {
-        int run = s_tot[e];
-        for (int cc = 0; cc < a.nchunks; ++cc) {
-            int* p = a.chunk + static_cast<size_t>(cc) * a.E + e;
-            const int n = *p;
-            *p = run;
-            run += n;
-        }
-    }
+    // LDS operations of one wave complete in order: lane 0's counts are seen.
+    for (int e = lane; e < a.E; e += 64) a.cnt[static_cast<size_t>(c) * a.E + e] = s_cnt[wv][e];
 }
+
+// ---------------------------------------------------------------------------
+// (2) Scan: workgroup e turns column e of the chunk counts into exclusive
+// prefixes and writes the expert's total.
+// ---------------------------------------------------------------------------
+constexpr int kScanThreads = 256;
+
+struct ScanArgs {
+    const int* cnt;  // [nchunks][E]
+    int* base;       // [nchunks][E] entries of the expert in earlier chunks
+    int* tot;        // [E]
+    int nchunks;
+    int E;
+};
+
+__global__ __launch_bounds__(kScanThreads) void moe_scan_kernel(const ScanArgs a) {
+    __shared__ int s_wave[kScanThreads / 64];
+    const int e = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    // Thread i owns chunks [i * per, (i + 1) * per).
+    const int per = (a.nchunks + kScanThreads - 1) / kScanThreads;
+    const int c0 = threadIdx.x * per;
+    const int c1 = min(c0 + per, a.nchunks);
+    int sum = 0;
+    for (int c = c0; c < c1; ++c) sum += a.cnt[static_cast<size_t>(c) * a.E + e];
+    const int x = wave_inclusive_scan(sum, lane);
+    if (lane == 63) s_wave[wv] = x;
+    __syncthreads();
+    int run = x - sum;
+    int total = 0;
+#pragma unroll
+    for (int w = 0; w < kScanThreads / 64; ++w) {
+        run += (w < wv) ? s_wave[w] : 0;
+        total += s_wave[w];
+    }
+    for (int c = c0; c < c1; ++c) {
+        const size_t i = static_cast<size_t>(c) * a.E + e;
+        const int v = a.cnt[i];
+        a.base[i] = run;
+        run += v;
+    }
+    if (threadIdx.x == 0) a.tot[e] = total;
+}
+
+// ---------------------------------------------------------------------------
+// (3) Permute.
+// ---------------------------------------------------------------------------
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kCopyBatch = 8;          // 16-byte loads per lane in flight before the stores
+constexpr int kPermuteWaves = 4;       // one token per wave
+constexpr int kLdsCounts = 4096;       // count matrices up to this size are scanned in LDS
 
 struct PermuteArgs {
     const int* ids;
     const int* rank;
-    const int* base;  // [nchunks][E] row bases
+    const int* cnt;   // [nchunks][E] counts; scanned in LDS when `base` is null
+    const int* base;  // [nchunks][E] prefixes from the scan kernel, or null
+    const int* tot;   // [E] totals from the scan kernel (with `base`)
     const uint16_t* x;
-    uint16_t* xp;
+    uint16_t* xp;     // null: index arrays only
+    int* counts;
+    int* offsets;
     int* inverse;
     int* sorted;
     int T;
     int E;
+    int nchunks;
     int hidden;
     int vec;  // 1: rows move as 16-byte vectors
 };
 
 template <int K>
-__global__ __launch_bounds__(256) void moe_permute_kernel(const PermuteArgs a) {
+__global__ __launch_bounds__(64 * kPermuteWaves) void moe_permute_kernel(const PermuteArgs a) {
+    __shared__ int s_base[kLdsCounts];  // [nchunks][E] exclusive prefixes over chunks
+    __shared__ int s_off[kMaxExperts];  // expert offsets
     const int lane = threadIdx.x & 63;
-    const int waves = gridDim.x * (blockDim.x >> 6);
-    for (int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); t < a.T; t += waves) {
-        const int c = t / kChunkTokens;
-        long long rows[K];
+    const int wv = threadIdx.x >> 6;
+    const int t = blockIdx.x * kPermuteWaves + wv;
+    const bool live = t < a.T;
+    const bool copy = live && a.xp != nullptr && a.vec;
+    const int nv = a.hidden / 8;
+    const u32x4* __restrict__ src =
+        reinterpret_cast<const u32x4*>(a.x + static_cast<size_t>(live ? t : 0) * a.hidden);
+
+    // The first batch of the row is loaded before the bookkeeping below, so
+    // its latency hides the scans.
+    u32x4 v[kCopyBatch];
+    if (copy) {
 #pragma unroll
-        for (int k = 0; k < K; ++k) {
-            const int e = a.ids[static_cast<size_t>(t) * K + k];
-            const int rk = a.rank[static_cast<size_t>(t) * K + k];
-            int row = -1;
-            if (e >= 0 && e < a.E && rk >= 0) row = a.base[static_cast<size_t>(c) * a.E + e] + rk;
-            rows[k] = row;
-            if (lane == 0) {
-                a.inverse[static_cast<size_t>(t) * K + k] = row;
-                if (row >= 0) a.sorted[row] = t;
+        for (int u = 0; u < kCopyBatch; ++u) {
+            const int i = 64 * u + lane;
+            if (i < nv) v[u] = src[i];
+        }
+    }
+
+    // Per-expert totals: from the scan kernel, or scanned here from the counts.
+    if (a.base == nullptr) {
+        const int n = a.nchunks * a.E;
+        for (int i = threadIdx.x; i < n; i += 64 * kPermuteWaves) s_base[i] = a.cnt[i];
+        __syncthreads();
+        // One wave per expert column, 64 chunks per step.
+        for (int e = wv; e < a.E; e += kPermuteWaves) {
+            int run = 0;
+            for (int c0 = 0; c0 < a.nchunks; c0 += 64) {
+                const int c = c0 + lane;
+                const int val = (c < a.nchunks) ? s_base[c * a.E + e] : 0;
+                const int x = wave_inclusive_scan(val, lane);
+                if (c < a.nchunks) s_base[c * a.E + e] = run + x - val;
+                run += __shfl(x, 63);
+            }
+            if (lane == 0) s_off[e] = run;
+        }
+    } else {
+        for (int e = threadIdx.x; e < a.E; e += 64 * kPermuteWaves) s_off[e] = a.tot[e];
+    }
+    __syncthreads();
+    // Expert offsets: exclusive scan of the totals; workgroup 0 also
+    // publishes counts and offsets.
+    if (wv == 0) {
+        int run = 0;
+        for (int e0 = 0; e0 < a.E; e0 += 64) {
+            const int e = e0 + lane;
+            const int val = (e < a.E) ? s_off[e] : 0;
+            const int x = wave_inclusive_scan(val, lane);
+            if (e < a.E) {
+                s_off[e] = run + x - val;
+                if (blockIdx.x == 0) {
+                    a.counts[e] = val;
+                    a.offsets[e] = run + x - val;
+                }
+            }
+            run += __shfl(x, 63);
+        }
+        if (blockIdx.x == 0 && lane == 0) a.offsets[a.E] = run;
+    }
+    __syncthreads();
+    if (!live) return;
+
+    const int c = t / kChunkTokens;
+    long long rows[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int e = a.ids[static_cast<size_t>(t) * K + k];
+        const int rk = a.rank[static_cast<size_t>(t) * K + k];
+        int row = -1;
+        if (e >= 0 && e < a.E && rk >= 0) {
+            const size_t ce = static_cast<size_t>(c) * a.E + e;
+            row = s_off[e] + (a.base != nullptr ? a.base[ce] : s_base[ce]) + rk;
+        }
+        rows[k] = row;
+        if (lane == 0) {
+            a.inverse[static_cast<size_t>(t) * K + k] = row;
+            if (row >= 0) a.sorted[row] = t;
+        }
+    }
+    if (a.xp == nullptr) return;
+    if (a.vec) {
+        for (int i0 = 0; i0 < nv; i0 += 64 * kCopyBatch) {
+            if (i0 > 0) {
+#pragma unroll
+                for (int u = 0; u < kCopyBatch; ++u) {
+                    const int i = i0 + 64 * u + lane;
+                    if (i < nv) v[u] = src[i];
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+                if (rows[k] < 0) continue;
+                u32x4* __restrict__ dst = reinterpret_cast<u32x4*>(a.xp + rows[k] * a.hidden);
+#pragma unroll
+                for (int u = 0; u < kCopyBatch; ++u) {
+                    const int i = i0 + 64 * u + lane;
+                    if (i < nv) __builtin_nontemporal_store(v[u], dst + i);
+                }
             }
         }
-        if (a.xp == nullptr) continue;
-        if (a.vec) {
-            const int nv = a.hidden / 8;
-            const uint4* src = reinterpret_cast<const uint4*>(a.x + static_cast<size_t>(t) * a.hidden);
-            for (int i = lane; i < nv; i += 64) {
-                const uint4 v = src[i];
+    } else {
+        const uint16_t* s16 = a.x + static_cast<size_t>(t) * a.hidden;
+        for (int i = lane; i < a.hidden; i += 64) {
+            const uint16_t val = s16[i];
 #pragma unroll
-                for (int k = 0; k < K; ++k) {
-                    if (rows[k] >= 0) {
-                        reinterpret_cast<uint4*>(a.xp + rows[k] * a.hidden)[i] = v;
-                    }
-                }
-            }
-        } else {
-            const uint16_t* src = a.x + static_cast<size_t>(t) * a.hidden;
-            for (int i = lane; i < a.hidden; i += 64) {
-                const uint16_t v = src[i];
-#pragma unroll
-                for (int k = 0; k < K; ++k) {
-                    if (rows[k] >= 0) a.xp[rows[k] * a.hidden + i] = v;
-                }
+            for (int k = 0; k < K; ++k) {
+                if (rows[k] >= 0) a.xp[rows[k] * a.hidden + i] = val;
             }
         }
     }
@@ -275,32 +450,35 @@ struct RouteLaunch {
 template <int K>
 struct RankLaunch {
     static hipError_t run(const RankArgs& a, hipStream_t s) {
-        const int grid = (a.nchunks + 3) / 4 > 0 ? (a.nchunks + 3) / 4 : 1;
-        return launch(moe_rank_kernel<K>, dim3(grid), dim3(256), 0, s, a);
+        const int grid = (a.nchunks + kRankWaves - 1) / kRankWaves;
+        return launch(moe_rank_kernel<K>, dim3(grid), dim3(64 * kRankWaves), 0, s, a);
     }
 };
 
 template <int K>
 struct PermuteLaunch {
     static hipError_t run(const PermuteArgs& a, hipStream_t s) {
-        const int wg = (a.T + 3) / 4;
-        const int grid = wg < 65536 ? (wg > 0 ? wg : 1) : 65536;
-        return launch(moe_permute_kernel<K>, dim3(grid), dim3(256), 0, s, a);
+        // One wave per token; at least one workgroup so counts and offsets
+        // are written when there are no tokens.
+        const int grid = a.T > 0 ? (a.T + kPermuteWaves - 1) / kPermuteWaves : 1;
+        return launch(moe_permute_kernel<K>, dim3(grid), dim3(64 * kPermuteWaves), 0, s, a);
     }
 };
 
 struct DispatchLayout {
     int nchunks;
-    size_t ticket, chunk, rank, total;
+    size_t cnt, base, tot, rank, total;
 };
 
 DispatchLayout dispatch_layout(int T, int E, int K) {
     DispatchLayout l{};
     l.nchunks = (T + kChunkTokens - 1) / kChunkTokens;
     auto up = [](size_t x) { return (x + 255) / 256 * 256; };
-    l.ticket = 0;
-    l.chunk = 256;
-    l.rank = l.chunk + up(sizeof(int) * static_cast<size_t>(l.nchunks) * E);
+    const size_t counts = sizeof(int) * static_cast<size_t>(l.nchunks) * E;
+    l.cnt = 0;
+    l.base = l.cnt + up(counts);
+    l.tot = l.base + up(counts);
+    l.rank = l.tot + up(sizeof(int) * static_cast<size_t>(E));
     l.total = l.rank + up(sizeof(int) * static_cast<size_t>(T) * K);
     return l;
 }
@@ -348,12 +526,18 @@ size_t swiftllm_hip_moe_dispatch_workspace_size(int num_tokens, int num_experts,
     return dispatch_layout(num_tokens, num_experts, top_k).total;
 }
 
-int swiftllm_hip_moe_dispatch(const int32_t* expert_ids, const void* x, int num_tokens, int top_k,
-                              int num_experts, int hidden, int32_t* expert_counts,
-                              int32_t* expert_offsets, void* x_perm, int32_t* inverse,
-                              int32_t* sorted_token_ids, void* workspace, size_t workspace_bytes,
-                              hipStream_t stream) {
-    const char* who = "swiftllm_hip_moe_dispatch";
+}  // extern "C"
+
+namespace swiftllm {
+namespace {
+
+// Shared body of the dispatch entry points. With `logits`, the rank kernel
+// routes each chunk first and writes expert_ids and weights.
+int dispatch(const char* who, const float* logits, int32_t* expert_ids, float* weights,
+             const void* x, int num_tokens, int top_k, int num_experts, int hidden,
+             int32_t* expert_counts, int32_t* expert_offsets, void* x_perm, int32_t* inverse,
+             int32_t* sorted_token_ids, void* workspace, size_t workspace_bytes,
+             hipStream_t stream) {
     int rc = validate_moe(who, num_tokens, num_experts, top_k);
     if (rc != SWIFTLLM_OK) return rc;
     if (hidden < 0 || (x_perm != nullptr && hidden == 0)) {
@@ -362,7 +546,8 @@ int swiftllm_hip_moe_dispatch(const int32_t* expert_ids, const void* x, int num_
     if (!expert_counts || !expert_offsets || !workspace) {
         return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: null pointer", who);
     }
-    if (num_tokens > 0 && (!expert_ids || !inverse || !sorted_token_ids || (x_perm && !x))) {
+    if (num_tokens > 0 && (!expert_ids || !inverse || !sorted_token_ids || (x_perm && !x) ||
+                           (logits && !weights))) {
         return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: null pointer", who);
     }
     const DispatchLayout l = dispatch_layout(num_tokens, num_experts, top_k);
@@ -376,31 +561,70 @@ int swiftllm_hip_moe_dispatch(const int32_t* expert_ids, const void* x, int num_
     }
     if ((rc = require_device()) != SWIFTLLM_OK) return rc;
     char* ws = static_cast<char*>(workspace);
-    RankArgs ra{};
-    ra.ids = expert_ids;
-    ra.rank = reinterpret_cast<int*>(ws + l.rank);
-    ra.chunk = reinterpret_cast<int*>(ws + l.chunk);
-    ra.counts = expert_counts;
-    ra.offsets = expert_offsets;
-    ra.ticket = reinterpret_cast<unsigned*>(ws + l.ticket);
-    ra.T = num_tokens;
-    ra.E = num_experts;
-    ra.nchunks = l.nchunks;
-    hipError_t err = by_k<RankLaunch>(top_k, ra, stream);
-    if (err != hipSuccess || num_tokens == 0) return launched(err, who);
+    int* cnt = reinterpret_cast<int*>(ws + l.cnt);
+    int* base = reinterpret_cast<int*>(ws + l.base);
+    int* tot = reinterpret_cast<int*>(ws + l.tot);
+    int* rank = reinterpret_cast<int*>(ws + l.rank);
+    if (num_tokens > 0) {
+        RankArgs ra{logits, expert_ids, weights, rank, cnt, num_tokens, num_experts, l.nchunks};
+        hipError_t err = by_k<RankLaunch>(top_k, ra, stream);
+        if (err != hipSuccess) return launched(err, who);
+    }
     PermuteArgs pa{};
+    pa.cnt = cnt;
+    if (static_cast<long long>(l.nchunks) * num_experts > kLdsCounts) {
+        ScanArgs sa{cnt, base, tot, l.nchunks, num_experts};
+        hipError_t err =
+            launch(moe_scan_kernel, dim3(num_experts), dim3(kScanThreads), 0, stream, sa);
+        if (err != hipSuccess) return launched(err, who);
+        pa.base = base;
+        pa.tot = tot;
+    }
     pa.ids = expert_ids;
-    pa.rank = ra.rank;
-    pa.base = ra.chunk;
+    pa.rank = rank;
     pa.x = static_cast<const uint16_t*>(x);
     pa.xp = static_cast<uint16_t*>(x_perm);
+    pa.counts = expert_counts;
+    pa.offsets = expert_offsets;
     pa.inverse = inverse;
     pa.sorted = sorted_token_ids;
     pa.T = num_tokens;
     pa.E = num_experts;
+    pa.nchunks = l.nchunks;
     pa.hidden = hidden;
     pa.vec = (hidden % 8 == 0) && (x_perm == nullptr || (aligned(x, 16) && aligned(x_perm, 16)));
     return launched(by_k<PermuteLaunch>(top_k, pa, stream), who);
+}
+
+}  // namespace
+}  // namespace swiftllm
+
+extern "C" {
+
+int swiftllm_hip_moe_dispatch(const int32_t* expert_ids, const void* x, int num_tokens, int top_k,
+                              int num_experts, int hidden, int32_t* expert_counts,
+                              int32_t* expert_offsets, void* x_perm, int32_t* inverse,
+                              int32_t* sorted_token_ids, void* workspace, size_t workspace_bytes,
+                              hipStream_t stream) {
+    return dispatch("swiftllm_hip_moe_dispatch", nullptr, const_cast<int32_t*>(expert_ids),
+                    nullptr, x, num_tokens, top_k, num_experts, hidden, expert_counts,
+                    expert_offsets, x_perm, inverse, sorted_token_ids, workspace, workspace_bytes,
+                    stream);
+}
+
+int swiftllm_hip_moe_route_dispatch(const float* logits, const void* x, int num_tokens,
+                                    int top_k, int num_experts, int hidden, int32_t* expert_ids,
+                                    float* weights, int32_t* expert_counts,
+                                    int32_t* expert_offsets, void* x_perm, int32_t* inverse,
+                                    int32_t* sorted_token_ids, void* workspace,
+                                    size_t workspace_bytes, hipStream_t stream) {
+    const char* who = "swiftllm_hip_moe_route_dispatch";
+    if (num_tokens > 0 && !logits) {
+        return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: null pointer", who);
+    }
+    return dispatch(who, logits, expert_ids, weights, x, num_tokens, top_k, num_experts, hidden,
+                    expert_counts, expert_offsets, x_perm, inverse, sorted_token_ids, workspace,
+                    workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -15,7 +15,7 @@ import numpy as np
 
 from . import _lib
 from ._hip import DeviceArray, Stream
-from .paged_attention import check_status, workspace
+from .paged_attention import check_status
 
 
 def moe_route(logits: DeviceArray, top_k: int, expert_ids: DeviceArray, weights: DeviceArray,
@@ -46,7 +46,8 @@ class DispatchBuffers:
     @classmethod
     def allocate(cls, num_tokens: int, num_experts: int, top_k: int, hidden: int,
                  with_rows: bool = True) -> "DispatchBuffers":
-        ws = workspace(moe_dispatch_workspace_size(num_tokens, num_experts, top_k))
+        n = moe_dispatch_workspace_size(num_tokens, num_experts, top_k)
+        ws = DeviceArray((max(n, 4) + 3) // 4, np.uint32)   # plain scratch
         return cls(
             counts=DeviceArray((num_experts,), np.int32),
             offsets=DeviceArray((num_experts + 1,), np.int32),
@@ -68,6 +69,21 @@ def moe_dispatch(expert_ids: DeviceArray, x: Optional[DeviceArray], num_experts:
         stream.handle if stream else None))
 
 
+def moe_route_dispatch(logits: DeviceArray, x: Optional[DeviceArray], top_k: int,
+                       expert_ids: DeviceArray, weights: DeviceArray, out: DispatchBuffers,
+                       stream: Optional[Stream] = None) -> None:
+    """moe_route then moe_dispatch in one call: the routing runs inside the
+    dispatch's ranking kernel."""
+    T, E = logits.shape
+    hidden = x.shape[1] if x is not None else 0
+    check_status(_lib.lib().swiftllm_hip_moe_route_dispatch(
+        logits.ptr, x.ptr if x is not None else None, T, top_k, E, hidden, expert_ids.ptr,
+        weights.ptr, out.counts.ptr, out.offsets.ptr,
+        out.x_perm.ptr if out.x_perm is not None else None, out.inverse.ptr,
+        out.sorted_token_ids.ptr, out.workspace.ptr, out.workspace.nbytes,
+        stream.handle if stream else None))
+
+
 class MoeRouting:
     """The routing half of MoeMlp (mlp.rs:209-221 fields num_experts,
     num_experts_per_tok): route(logits) then dispatch(x)."""
@@ -82,7 +98,6 @@ class MoeRouting:
         K = self.num_experts_per_tok
         ids = DeviceArray((T, K), np.int32)
         w = DeviceArray((T, K), np.float32)
-        moe_route(router_logits, K, ids, w, stream)
         bufs = DispatchBuffers.allocate(T, self.num_experts, K, x.shape[1])
-        moe_dispatch(ids, x, self.num_experts, bufs, stream)
+        moe_route_dispatch(router_logits, x, K, ids, w, bufs, stream)
         return ids, w, bufs
