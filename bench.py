@@ -1,8 +1,8 @@
 #!/usr/bin/env python3
 """Benchmark of the paged-attention decode hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--variant v2|v1]
-                    [--partition P] [--rotate R] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2|3|4|5]
+                    [--variant v2|v1] [--partition P] [--rotate R] [--no-cpu]
 
 Workload: Llama-3-8B layer decode (32 query heads, 8 kv heads, head_dim 128,
 block_size 16, batch 64, context lengths uniform in [512, 4096], randomly
@@ -15,6 +15,11 @@ Infinity Cache.
 Prints one JSON line: the metric (KV-read GB/s), us/call, the roofline of the
 decode kernel (algorithmic bytes / kernel time vs the 8 TB/s HBM peak) and the
 fp32 CPU restatement timed on this host as a reference point.
+
+The other configurations are measured the same way: --config 3 (8 sequences
+of 32768 tokens, 64 query heads, split-K), --config 4 (a ragged step: cache
+write of 256 new tokens, then decode) and --config 5 (MoE top-2 routing and
+dispatch of 4096 tokens, hidden 4096, 8 experts).
 """
 
 from __future__ import annotations
@@ -43,8 +48,10 @@ def parse():
                     help="2: Llama-3-8B decode (the metric's workload); 3: long-context split-K; "
                          "4: ragged step (cache write + decode); 5: MoE route + dispatch")
     ap.add_argument("--variant", choices=["v1", "v2"], default=None,
-                    help="default: v1 for configs 2 and 4, v2 for config 3")
-    ap.add_argument("--partition", type=int, default=512)
+                    help="default: v1 for config 2, v2 for configs 3 and 4")
+    ap.add_argument("--partition", type=int, default=None,
+                    help="v2 partition size in tokens, 0 = balanced (stream-K) scheduling; "
+                         "default 4096 for config 3, 0 for config 4")
     ap.add_argument("--rotate", type=int, default=None,
                     help="input copies rotated between calls (default 4 for decode, 8 for MoE)")
     ap.add_argument("--seed", type=int, default=0)
@@ -79,7 +86,9 @@ def main():
     if args.rotate is None:
         args.rotate = 4
     if args.variant is None:
-        args.variant = "v2" if args.config == 3 else "v1"
+        args.variant = "v1" if args.config == 2 else "v2"
+    if args.partition is None:
+        args.partition = 4096 if args.config == 3 else 0
     t0 = time.time()
     w = workloads.decode_config(args.config, seed=args.seed)
     sh = w.shape
@@ -336,7 +345,7 @@ def bench_moe(args):
         "config": {"workload": "mixtral-8x7b-moe-dispatch", "num_tokens": T, "hidden": hidden,
                    "num_experts": E, "top_k": K, "copies_rotated": copies,
                    "algorithmic_bytes_per_call": alg,
-                   "entry": "swiftllm_hip_moe_route_dispatch (rank with routing, scan, permute)"},
+                   "entry": "swiftllm_hip_moe_route_dispatch (rank with routing, then permute)"},
         "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(value / HBM_PEAK_GBS, 4),
                      "traffic": read_traffic("moe_config5_traffic.json")},
