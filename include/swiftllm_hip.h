@@ -103,7 +103,14 @@ void launch_reshape_and_cache(void* key, void* value, void* key_cache,
  * partition and keeps (max logit, exp sum, partial output) in `workspace`;
  * a second kernel rescales and reduces the partitions of every sequence
  * that has more than one (a sequence with a single partition is written by
- * the first kernel directly). `workspace` holds at least
+ * the first kernel directly).
+ * partition_size 0 selects balanced scheduling instead: the blocks of all
+ * sequences are split into equal ranges, one per team of waves, so a ragged
+ * batch has no long tail; ranges that cut a sequence leave fragments that a
+ * second kernel combines. Shapes it cannot take (more than 4096 sequences,
+ * or teams so wide that fewer than four fit in the resident grid) fall back
+ * to partitions of 512 tokens; the workspace size query covers both.
+ * `workspace` holds at least
  * swiftllm_hip_paged_attention_v2_workspace_size() bytes, 256-byte aligned;
  * it is plain scratch (no initialisation, contents unspecified after the
  * call). Calls that share a workspace must be ordered on one stream. */
