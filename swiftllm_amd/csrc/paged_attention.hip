@@ -66,6 +66,7 @@ struct DecodeArgs {
     int num_blocks;   // bound on block ids; <= 0: unbounded
     int part_blocks;  // blocks per partition; 0: single pass
     int MP;           // partitions per sequence in the workspace
+    int snake;        // > 0: single-pass item order in snake rounds of this many
 };
 
 __device__ __forceinline__ f4 mfma16(h4 a, h4 b, f4 c) {
@@ -285,8 +286,11 @@ __device__ __forceinline__ int sequence_for_block(const int* ctx, int S, int r) 
     return s_seq;
 }
 
+// At least two waves per SIMD: caps the registers (at 157 VGPRs for D=128 the
+// kernel fits three waves per SIMD), so several workgroups share a CU.
 template <int D, int NW>
-__global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeArgs a) {
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void paged_decode_kernel(const DecodeArgs a) {
     constexpr int NJ = D / 16;
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -294,9 +298,29 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeArgs 
     const int kg = lane >> 4;  // MFMA k-group: 4 consecutive k per lane
 
     const int part = blockIdx.x;
-    const int kvh = blockIdx.y / a.nhc;
-    const int hc = blockIdx.y - kvh * a.nhc;
-    const int s = sequence_for_block(a.ctx, gridDim.z, blockIdx.z);
+    int kvh, hc, s;
+    if (a.snake > 0) {
+        // Single pass, whole grid resident: workgroup i takes item
+        // snake(i) of the longest-first list of (sequence, kv head, head
+        // chunk) items, where the list is cut into rounds of `snake`
+        // items and every other round runs backwards. Workgroups i and
+        // i + snake, which the dispatcher puts on the same CU, then pair a
+        // long sequence with a short one.
+        const int HC = gridDim.y;
+        const int i = blockIdx.z * HC + blockIdx.y;
+        const int k = i / a.snake;
+        const int pos = i - k * a.snake;
+        const int rlen = min(a.snake, static_cast<int>(gridDim.z) * HC - k * a.snake);
+        const int item = k * a.snake + ((k & 1) ? (rlen - 1 - pos) : pos);
+        const int sub = item % HC;
+        kvh = sub / a.nhc;
+        hc = sub - kvh * a.nhc;
+        s = sequence_for_block(a.ctx, gridDim.z, item / HC);
+    } else {
+        kvh = blockIdx.y / a.nhc;
+        hc = blockIdx.y - kvh * a.nhc;
+        s = sequence_for_block(a.ctx, gridDim.z, blockIdx.z);
+    }
     const int g0 = hc * 16;
     const int gn = min(16, a.G - g0);  // query heads served here
     const int gstride = min(16, a.G);  // LDS rows per wave
@@ -962,7 +986,7 @@ int validate_decode(const char* who, const void* out, const void* q, const void*
 // Waves per workgroup of the single-pass kernel: the whole context of a
 // (sequence, kv head) is one workgroup, so it gets the most waves.
 #ifndef SWIFTLLM_WAVES_V1
-#define SWIFTLLM_WAVES_V1 8
+#define SWIFTLLM_WAVES_V1 4
 #endif
 constexpr int kWavesV1 = SWIFTLLM_WAVES_V1;
 // Waves per workgroup of a split-K partition.
@@ -1005,6 +1029,8 @@ DecodeArgs make_args(void* out, const void* q, const void* kc, const void* vc, c
     return a;
 }
 
+int device_cus();
+
 int decode_v1(void* out, const void* q, const void* kc, const void* vc, const int* bt,
               const int* ctx, float scale, const Shape& sh, int num_blocks, hipStream_t stream,
               const char* who) {
@@ -1015,6 +1041,12 @@ int decode_v1(void* out, const void* q, const void* kc, const void* vc, const in
     DecodeArgs a = make_args(out, q, kc, vc, bt, ctx, scale, sh, num_blocks);
     a.part_blocks = 0;
     a.MP = 1;
+    // Snake order when the whole grid is resident at once (three 4-wave
+    // workgroups per CU at the kernel's register count) and sequences are
+    // ranked; otherwise plain longest-first order for the dispatcher to
+    // balance dynamically.
+    const long long items = static_cast<long long>(sh.S) * a.Hkv * a.nhc;
+    a.snake = (kWavesV1 == 4 && sh.S <= kLptMaxSeqs && items <= 3LL * device_cus()) ? device_cus() : 0;
     return launched(launch_decode<kWavesV1>(a, sh.D, sh.S, 1, stream), who);
 }
 
