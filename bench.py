@@ -44,9 +44,10 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", type=int, choices=[2, 3, 4, 5], default=2,
+    ap.add_argument("--config", type=int, choices=[2, 3, 4, 5, 6, 7], default=2,
                     help="2: Llama-3-8B decode (the metric's workload); 3: long-context split-K; "
-                         "4: ragged step (cache write + decode); 5: MoE route + dispatch")
+                         "4: ragged step (cache write + decode); 5: MoE route + dispatch; "
+                         "6: copy_blocks (copy-on-write, 32 layers); 7: swap_blocks out and in")
     ap.add_argument("--variant", choices=["v1", "v2"], default=None,
                     help="default: v1 for config 2, v2 for configs 3 and 4")
     ap.add_argument("--partition", type=int, default=None,
@@ -83,6 +84,8 @@ def main():
         calibrate(args.calib_copy_mib << 20)
     if args.config == 5:
         return bench_moe(args)
+    if args.config in (6, 7):
+        return bench_blocks(args)
     if args.rotate is None:
         args.rotate = 4
     if args.variant is None:
@@ -350,6 +353,79 @@ def bench_moe(args):
                      "frac": round(value / HBM_PEAK_GBS, 4),
                      "traffic": read_traffic("moe_config5_traffic.json")},
         "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+def bench_blocks(args):
+    """Config 6: copy-on-write of 128 block pairs in the K and V caches of 32
+    Llama-3-8B layers (8 kv heads, head_dim 128, block_size 16: 32 KiB per
+    block and array, 256 MiB read + 256 MiB written per call), two mappings
+    alternating. Config 7: swap-out of 1024 blocks of one such cache array to
+    pinned host memory and swap-in of 1024 others (32 MiB each way)."""
+    from swiftllm_amd import paged_attention as pa
+    from swiftllm_amd._hip import DeviceArray, HostArray, Stream
+
+    stream = Stream()
+    Hkv, D, BS = 8, 128, 16
+    block = Hkv * D * BS * 2
+    rng = np.random.default_rng(args.seed)
+    if args.config == 6:
+        layers, NB, pairs = 32, 1024, 128
+        kcs = [DeviceArray((NB * block // 4,), np.uint32) for _ in range(layers)]
+        vcs = [DeviceArray((NB * block // 4,), np.uint32) for _ in range(layers)]
+        for c in kcs + vcs:
+            c.fill_byte(0x3C)
+        maps = []
+        for _ in range(2):
+            ids = rng.permutation(NB)[:2 * pairs]
+            maps.append(DeviceArray.from_numpy(np.stack([ids[:pairs], ids[pairs:]], 1).astype(np.int64)))
+
+        def step(i):
+            pa.copy_blocks(kcs, vcs, maps[i % 2], pairs, Hkv, D, BS, stream)
+
+        moved = pairs * 2 * layers * block
+        alg = 2 * moved
+        work = {"workload": "copy-blocks-cow", "layers": layers, "pairs": pairs,
+                "block_bytes_per_array": block, "pool_blocks": NB, "mappings_alternated": 2,
+                "algorithmic_bytes_per_call": alg}
+        metric = "copy_blocks GB/s (bytes read + written) @ 32 Llama-3-8B layers"
+        roof = {"bound": "hbm", "peak": HBM_PEAK_GBS}
+    else:
+        nblk, NBD, NBH = 1024, 4096, 4096
+        dev = DeviceArray((NBD * block // 4,), np.uint32)
+        host = HostArray((NBH * block // 4,), np.uint32)
+        dev.fill_byte(0x3C)
+        host.array()[...] = 0x3C3C3C3C
+        out_map = DeviceArray.from_numpy(np.stack([rng.permutation(NBD)[:nblk],
+                                                   rng.permutation(NBH)[:nblk]], 1).astype(np.int64))
+        in_map = DeviceArray.from_numpy(np.stack([rng.permutation(NBH)[:nblk],
+                                                  rng.permutation(NBD)[:nblk]], 1).astype(np.int64))
+
+        def step(i):
+            pa.swap_blocks(dev, host, out_map, nblk, block, stream)
+            pa.swap_blocks(host, dev, in_map, nblk, block, stream)
+
+        alg = 2 * nblk * block
+        work = {"workload": "swap-blocks-out-in", "blocks_each_way": nblk, "block_bytes": block,
+                "host_memory": "hipHostMalloc pinned", "algorithmic_bytes_per_call": alg}
+        metric = "swap_blocks GB/s over the host link (out + in) @ Llama-3-8B blocks"
+        # PCIe 5.0 x16 moves 64 GB/s each way; out and in run one after the other.
+        roof = {"bound": "pcie", "peak": 64.0}
+    # A swap call takes about a millisecond: fewer steps keep the run short.
+    steps = args.steps if args.config == 6 else max(args.steps // 20, 5)
+    warmup = args.warmup if args.config == 6 else 3
+    ms, p10, p50, p90 = timed(step, stream, steps, warmup, args.samples if args.config == 6 else 0)
+    value = alg / (ms * 1e-3) / 1e9
+    rec = {
+        "metric": metric, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps,
+        "warmup": warmup, "ms_per_step": round(ms, 6), "us_per_call": round(ms * 1e3, 3),
+        "us_per_call_p10_p50_p90": [round(p10, 2), round(p50, 2), round(p90, 2)],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8 (bit copies)",
+        "data": "synthetic (filled pools)", "config": work,
+        "roofline": dict(roof, achieved=round(value, 2), unit="GB/s",
+                         frac=round(value / roof["peak"], 4), traffic=None),
+        "cpu_baseline": None,
     }
     print(json.dumps(rec), flush=True)
 

@@ -200,6 +200,56 @@ int swiftllm_hip_reshape_and_cache(const void* key, const void* value,
                                    hipStream_t stream);
 
 /* ------------------------------------------------------------------------ */
+/* 3b. Block copies of the KV cache. block_mapping holds num_pairs (src, dst) */
+/*     int64 pairs in memory the device can read (device memory or pinned    */
+/*     host memory). A pair with a negative id is skipped; destinations must */
+/*     be distinct and must not be sources in the same call.                 */
+/* ------------------------------------------------------------------------ */
+
+/* Replaces launch_copy_blocks (paged_attention.cu:302-327; kernel cu:201-227,
+ * whose 2048-thread workgroups fail to launch): K[dst] = K[src] and
+ * V[dst] = V[src] for whole [Hkv, D, BS] blocks, one launch. */
+void launch_copy_blocks(int64_t* block_mapping, void* key_cache,
+                        void* value_cache, int num_pairs, int num_kv_heads,
+                        int head_dim, int block_size, hipStream_t stream);
+
+/* Status twin of launch_copy_blocks; ids outside [0, num_blocks) are skipped
+ * (num_blocks <= 0: no bound). */
+int swiftllm_hip_launch_copy_blocks(const int64_t* block_mapping,
+                                    void* key_cache, void* value_cache,
+                                    int num_pairs, int num_kv_heads,
+                                    int head_dim, int block_size,
+                                    int num_blocks, hipStream_t stream);
+
+/* Replaces bindings::copy_blocks (bindings.rs:200-223): the same pairs in
+ * the K and V caches of every layer. key_caches / value_caches are host
+ * arrays of num_layers device pointers. */
+int swiftllm_hip_copy_blocks(void* const* key_caches,
+                             void* const* value_caches,
+                             const int64_t* block_mapping, size_t num_pairs,
+                             size_t num_layers, size_t num_kv_heads,
+                             size_t head_dim, size_t block_size,
+                             hipStream_t stream);
+
+/* Replaces bindings::swap_blocks (bindings.rs:225-242):
+ * dst[dst_id * block_size_bytes, + block_size_bytes) =
+ * src[src_id * block_size_bytes, + block_size_bytes) for every pair. src
+ * and dst are device memory or pinned host memory (hipHostMalloc), in any
+ * combination; one kernel moves every block. */
+int swiftllm_hip_swap_blocks(const void* src, void* dst,
+                             const int64_t* block_mapping, size_t num_pairs,
+                             size_t block_size_bytes, hipStream_t stream);
+
+/* swiftllm_hip_swap_blocks with pool bounds: pairs whose src id is outside
+ * [0, src_blocks) or whose dst id is outside [0, dst_blocks) are skipped
+ * (a bound <= 0: none). */
+int swiftllm_hip_launch_swap_blocks(const void* src, void* dst,
+                                    const int64_t* block_mapping,
+                                    size_t num_pairs, size_t block_size_bytes,
+                                    long long src_blocks, long long dst_blocks,
+                                    hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
 /* 4. MoE top-k routing and dispatch. The reference has no kernel for this:  */
 /*    MoeMlp::forward (crates/swiftllm-models/src/layers/mlp.rs:240-252)     */
 /*    names the steps (router logits, top-k, route, combine) and returns     */

@@ -17,6 +17,8 @@ reference repository; "cu:" = crates/swiftllm-cuda/kernels/paged_attention.cu):
   moe_route / moe_dispatch   mlp.rs:240-246 steps with sampling/mod.rs:366-385
                              conventions (max-subtracted softmax, stable
                              descending order)
+  copy_blocks / swap_blocks  numpy: cu:201-227 (launcher cu:302-327) and
+                             crates/swiftllm-cuda/src/bindings.rs:200-242
 
 Which independent checks pin each function is stated in the tests that use
 it (tests/test_oracle_*.py); every function here has at least one.
@@ -153,6 +155,29 @@ def reshape_and_cache_numpy(key, value, kc, vc, slot_mapping) -> None:
     b, o = sm[t] // BS, sm[t] % BS
     kc[b, :, :, o] = key[t]
     vc[b, :, :, o] = value[t]
+
+
+def copy_blocks(key_caches, value_caches, block_mapping) -> None:
+    """cu:201-227 (and the per-layer form of bindings.rs:200-223), in place:
+    for each (src, dst) pair, the whole [Hkv, D, BS] block of every K and V
+    cache is copied from src to dst. Pairs with a negative id are skipped."""
+    for src, dst in np.asarray(block_mapping, dtype=np.int64).reshape(-1, 2):
+        if src < 0 or dst < 0:
+            continue
+        for c in list(key_caches) + list(value_caches):
+            c[dst] = c[src]
+
+
+def swap_blocks(src, dst, block_mapping, block_size_bytes: int) -> None:
+    """bindings.rs:225-242 on byte views, in place: block dst_id of `dst`
+    takes the block_size_bytes bytes of block src_id of `src`."""
+    s8 = np.asarray(src).reshape(-1).view(np.uint8)
+    d8 = dst.reshape(-1).view(np.uint8)
+    n = block_size_bytes
+    for a, b in np.asarray(block_mapping, dtype=np.int64).reshape(-1, 2):
+        if a < 0 or b < 0:
+            continue
+        d8[b * n:(b + 1) * n] = s8[a * n:(a + 1) * n]
 
 
 def blocks_needed(num_tokens: int, block_size: int) -> int:

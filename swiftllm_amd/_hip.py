@@ -54,6 +54,8 @@ def hip() -> ctypes.CDLL:
             "hipSetDevice": [ctypes.c_int],
             "hipDeviceGetAttribute": [ctypes.POINTER(ctypes.c_int), ctypes.c_int, ctypes.c_int],
             "hipMemGetInfo": [ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)],
+            "hipHostMalloc": [ctypes.POINTER(vp), ctypes.c_size_t, ctypes.c_uint],
+            "hipHostFree": [vp],
         }.items():
             fn = getattr(h, name)
             fn.restype = ctypes.c_int
@@ -134,6 +136,41 @@ class DeviceArray:
     def free(self) -> None:
         if self._ptr:
             self._hip.hipFree(self._ptr)
+            self._ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class HostArray:
+    """Pinned host memory (hipHostMalloc) that kernels can address directly,
+    with a numpy view of it."""
+
+    def __init__(self, shape, dtype):
+        self.shape = tuple(int(s) for s in np.atleast_1d(shape)) if np.ndim(shape) else (int(shape),)
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        p = ctypes.c_void_p()
+        check(hip().hipHostMalloc(ctypes.byref(p), max(self.nbytes, 1), 0),
+              f"hipHostMalloc({self.nbytes})")
+        self._ptr = p.value
+        self._hip = hip()
+
+    @property
+    def ptr(self) -> int:
+        return self._ptr
+
+    def array(self) -> np.ndarray:
+        """numpy view of the pinned buffer (valid while this object lives)."""
+        buf = (ctypes.c_uint8 * max(self.nbytes, 1)).from_address(self._ptr)
+        return np.frombuffer(buf, dtype=np.uint8, count=self.nbytes).view(self.dtype).reshape(self.shape)
+
+    def free(self) -> None:
+        if self._ptr:
+            self._hip.hipHostFree(self._ptr)
             self._ptr = None
 
     def __del__(self):

@@ -15,6 +15,7 @@ _LIB: Optional[ctypes.CDLL] = None
 vp = ctypes.c_void_p
 i32 = ctypes.c_int
 sz = ctypes.c_size_t
+i64 = ctypes.c_longlong
 f32 = ctypes.c_float
 
 
@@ -66,6 +67,11 @@ SIGNATURES = {
         i32, [vp, vp, vp, vp, vp, ctypes.POINTER(ReshapeCacheParams), vp]),
     "swiftllm_hip_moe_route": (i32, [vp, i32, i32, i32, vp, vp, vp]),
     "swiftllm_hip_moe_dispatch_workspace_size": (sz, [i32, i32, i32]),
+    "launch_copy_blocks": (None, [vp, vp, vp, i32, i32, i32, i32, vp]),
+    "swiftllm_hip_launch_copy_blocks": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, vp]),
+    "swiftllm_hip_copy_blocks": (i32, [vp, vp, vp, sz, sz, sz, sz, sz, vp]),
+    "swiftllm_hip_swap_blocks": (i32, [vp, vp, vp, sz, sz, vp]),
+    "swiftllm_hip_launch_swap_blocks": (i32, [vp, vp, vp, sz, sz, i64, i64, vp]),
     "swiftllm_hip_moe_dispatch": (
         i32, [vp, vp, i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, sz, vp]),
     "swiftllm_hip_moe_route_dispatch": (

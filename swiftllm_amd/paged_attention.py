@@ -2,10 +2,11 @@
 
 Reference (paths relative to the swiftllm repository):
   crates/swiftllm-cuda/src/lib.rs:16-42          CudaError variants
-  crates/swiftllm-cuda/src/bindings.rs:8-113     PagedAttentionParams,
+  crates/swiftllm-cuda/src/bindings.rs:8-242     PagedAttentionParams,
                                                  paged_attention_decode,
                                                  ReshapeCacheParams,
-                                                 reshape_and_cache
+                                                 reshape_and_cache,
+                                                 copy_blocks, swap_blocks
   crates/swiftllm-core/src/memory/paged_attention.rs:18-266
                                                  PagedAttentionConfig,
                                                  PagedAttention
@@ -28,9 +29,9 @@ from typing import Optional, Sequence, Union
 import numpy as np
 
 from . import _lib
-from ._hip import DeviceArray, Stream
+from ._hip import DeviceArray, HostArray, Stream
 
-Ptr = Union[int, DeviceArray, None]
+Ptr = Union[int, DeviceArray, HostArray, None]
 
 
 # ---------------------------------------------------------------------------
@@ -84,7 +85,7 @@ def check_status(status: int) -> None:
 def _p(x: Ptr) -> Optional[int]:
     if x is None:
         return None
-    if isinstance(x, DeviceArray):
+    if isinstance(x, (DeviceArray, HostArray)):
         return x.ptr
     return int(x)
 
@@ -145,10 +146,50 @@ def reshape_and_cache(key: Ptr, value: Ptr, key_cache: Ptr, value_cache: Ptr, sl
         _s(stream)))
 
 
+def copy_blocks(key_caches: Sequence[Ptr], value_caches: Sequence[Ptr], block_mapping: Ptr,
+                num_pairs: int, num_kv_heads: int, head_dim: int, block_size: int,
+                stream: Optional[Stream] = None) -> None:
+    """bindings.rs:200-223: the (src, dst) int64 pairs of block_mapping in the
+    K and V caches of every layer (one device pointer per layer)."""
+    n = len(key_caches)
+    if len(value_caches) != n:
+        raise InvalidParameter(f"{n} key caches but {len(value_caches)} value caches")
+    kc = (ctypes.c_void_p * max(n, 1))(*[_p(k) for k in key_caches])
+    vc = (ctypes.c_void_p * max(n, 1))(*[_p(v) for v in value_caches])
+    check_status(_lib.lib().swiftllm_hip_copy_blocks(
+        ctypes.cast(kc, ctypes.c_void_p), ctypes.cast(vc, ctypes.c_void_p), _p(block_mapping),
+        num_pairs, n, num_kv_heads, head_dim, block_size, _s(stream)))
+
+
+def swap_blocks(src: Ptr, dst: Ptr, block_mapping: Ptr, num_pairs: int, block_size_bytes: int,
+                stream: Optional[Stream] = None) -> None:
+    """bindings.rs:225-242: block copies between device memory and pinned host
+    memory (either side may be either)."""
+    check_status(_lib.lib().swiftllm_hip_swap_blocks(
+        _p(src), _p(dst), _p(block_mapping), num_pairs, block_size_bytes, _s(stream)))
+
+
 # ---------------------------------------------------------------------------
-# Launcher-level calls (paged_attention.cu:230-300 names plus the split-K and
+# Launcher-level calls (paged_attention.cu:230-327 names plus the split-K and
 # MoE extensions), status-checked.
 # ---------------------------------------------------------------------------
+def launch_copy_blocks(block_mapping: Ptr, key_cache: Ptr, value_cache: Ptr, num_pairs: int,
+                       num_kv_heads: int, head_dim: int, block_size: int, num_blocks: int = 0,
+                       stream: Optional[Stream] = None) -> None:
+    """launch_copy_blocks (paged_attention.cu:302-327) with a pool bound."""
+    check_status(_lib.lib().swiftllm_hip_launch_copy_blocks(
+        _p(block_mapping), _p(key_cache), _p(value_cache), num_pairs, num_kv_heads, head_dim,
+        block_size, num_blocks, _s(stream)))
+
+
+def launch_swap_blocks(src: Ptr, dst: Ptr, block_mapping: Ptr, num_pairs: int,
+                       block_size_bytes: int, src_blocks: int = 0, dst_blocks: int = 0,
+                       stream: Optional[Stream] = None) -> None:
+    check_status(_lib.lib().swiftllm_hip_launch_swap_blocks(
+        _p(src), _p(dst), _p(block_mapping), num_pairs, block_size_bytes, src_blocks,
+        dst_blocks, _s(stream)))
+
+
 def paged_attention_v1(output: Ptr, query: Ptr, key_cache: Ptr, value_cache: Ptr,
                        block_tables: Ptr, context_lens: Ptr, scale: float, num_seqs: int,
                        num_heads: int, num_kv_heads: int, head_dim: int, block_size: int,

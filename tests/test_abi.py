@@ -147,3 +147,35 @@ def test_device_not_found_without_gpu():
     with pytest.raises(pa.DeviceNotFound):
         pa.paged_attention_decode(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
                                   pa.PagedAttentionParams(2, 32, 8, 128, 16, 0.1, 64))
+
+
+def test_copy_blocks_dropin_argument_list():
+    """launch_copy_blocks keeps the parameter list of paged_attention.cu:302-311."""
+    text = HEADER.read_text()
+    cb = re.search(r"void launch_copy_blocks\((.*?)\);", text, flags=re.S).group(1)
+    params = [p.strip().split()[-1].lstrip("*") for p in cb.split(",")]
+    assert params == ["block_mapping", "key_cache", "value_cache", "num_pairs", "num_kv_heads",
+                      "head_dim", "block_size", "stream"]
+
+
+def test_block_copy_validation():
+    L = _lib.lib()
+    # null cache list / null mapping / misaligned mapping / bad sizes
+    assert L.swiftllm_hip_copy_blocks(None, None, FAKE, 2, 1, 8, 128, 16, None) == INVALID
+    kc = (ctypes.c_void_p * 1)(FAKE)
+    assert L.swiftllm_hip_copy_blocks(kc, kc, None, 2, 1, 8, 128, 16, None) == INVALID
+    assert L.swiftllm_hip_launch_copy_blocks(FAKE + 4, FAKE, FAKE, 2, 8, 128, 16, 0, None) == INVALID
+    assert L.swiftllm_hip_launch_copy_blocks(FAKE, FAKE, FAKE, 2, 0, 128, 16, 0, None) == INVALID
+    assert L.swiftllm_hip_launch_copy_blocks(FAKE, FAKE, FAKE, -1, 8, 128, 16, 0, None) == INVALID
+    assert L.swiftllm_hip_swap_blocks(FAKE, None, FAKE, 3, 4096, None) == INVALID
+    assert L.swiftllm_hip_swap_blocks(FAKE, FAKE, FAKE, 3, 0, None) == INVALID
+    L.launch_copy_blocks(FAKE, None, FAKE, 2, 8, 128, 16, None)
+    assert L.swiftllm_hip_last_error() == INVALID
+
+
+@pytest.mark.skipif(_hip.device_count() > 0, reason="checks the no-device path")
+def test_block_copies_without_gpu():
+    L = _lib.lib()
+    kc = (ctypes.c_void_p * 1)(FAKE)
+    assert L.swiftllm_hip_copy_blocks(kc, kc, FAKE, 2, 1, 8, 128, 16, None) == NODEV
+    assert L.swiftllm_hip_swap_blocks(FAKE, FAKE, FAKE, 3, 4096, None) == NODEV

@@ -28,7 +28,9 @@ def test_config1_tiny_mha(dev, variant, ps):
     assert_attention_close(out, _ref(w), f"config1 {variant} ps={ps}")
 
 
-@pytest.mark.parametrize("variant,ps", [("v1", None), ("v2", 512), ("v2", 0)])
+# 512: one wave per partition; 1024: two; 2048: the whole 4-wave workgroup
+@pytest.mark.parametrize("variant,ps", [("v1", None), ("v2", 512), ("v2", 1024), ("v2", 2048),
+                                        ("v2", 0)])
 def test_config2_llama3_8b(dev, variant, ps):
     w = workloads.decode_config(2, seed=2)
     out = DeviceWorkload(w).run(variant, partition_size=ps)
@@ -46,6 +48,8 @@ def test_config3_long_context_split_k(dev):
     # single pass and balanced scheduling agree with the oracle as well
     assert_attention_close(dw.run("v1"), ref, "config3 v1")
     assert_attention_close(dw.run("v2", partition_size=0), ref, "config3 balanced")
+    for ps in (1024, 4096):
+        assert_attention_close(dw.run("v2", partition_size=ps), ref, f"config3 v2/{ps}")
 
 
 def test_config4_ragged_step(dev):

@@ -167,3 +167,54 @@ def test_dispatch_drops_out_of_range_ids():
     assert counts.tolist() == [2, 2, 0, 0]
     assert inverse.tolist() == [[0, -1], [-1, 2], [3, 1]]
     assert sorted_ids.tolist() == [0, 2, 1, 2]
+
+
+def _tagged_pool(NB, Hkv, D, BS, salt):
+    b, h, d, t = np.meshgrid(np.arange(NB), np.arange(Hkv), np.arange(D), np.arange(BS),
+                             indexing="ij")
+    return ((b * 7919 + h * 211 + d * 17 + t + salt) % 65000 + 1).astype(np.uint16)
+
+
+def test_copy_blocks_tagged_pool():
+    """Every element of a destination block carries the tag of the same
+    (head, d, t) in its source block; every other block keeps its own tags."""
+    NB, Hkv, D, BS = 12, 2, 32, 16
+    layers = 3
+    kcs = [_tagged_pool(NB, Hkv, D, BS, 100 * l) for l in range(layers)]
+    vcs = [_tagged_pool(NB, Hkv, D, BS, 100 * l + 50) for l in range(layers)]
+    before_k = [k.copy() for k in kcs]
+    before_v = [v.copy() for v in vcs]
+    mapping = np.array([[1, 7], [4, 9], [-1, 3], [2, 11]], np.int64)
+    oracle.copy_blocks(kcs, vcs, mapping)
+    moved = {7: 1, 9: 4, 11: 2}
+    for l in range(layers):
+        for b in range(NB):
+            src = moved.get(b, b)
+            assert np.array_equal(kcs[l][b], before_k[l][src])
+            assert np.array_equal(vcs[l][b], before_v[l][src])
+
+
+def test_planted_swapped_pair_order_is_caught():
+    """Reading the pair as (dst, src) moves the wrong block."""
+    NB, Hkv, D, BS = 6, 1, 16, 16
+    kc = _tagged_pool(NB, Hkv, D, BS, 0)
+    ref = kc.copy()
+    oracle.copy_blocks([ref], [], np.array([[1, 4]], np.int64))
+    planted = kc.copy()
+    planted[1] = planted[4]
+    assert not np.array_equal(planted, ref)
+
+
+def test_swap_blocks_matches_byte_loop():
+    rng = np.random.default_rng(7)
+    nbytes, NS, ND = 40, 9, 6
+    src = rng.integers(0, 256, size=NS * nbytes, dtype=np.uint8)
+    dst = rng.integers(0, 256, size=ND * nbytes, dtype=np.uint8)
+    mapping = np.array([[8, 0], [3, 5], [0, -1], [5, 2]], np.int64)
+    expect = dst.copy()
+    for a, b in mapping:
+        if a >= 0 and b >= 0:
+            for i in range(nbytes):
+                expect[b * nbytes + i] = src[a * nbytes + i]
+    oracle.swap_blocks(src, dst, mapping, nbytes)
+    assert np.array_equal(dst, expect)
