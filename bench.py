@@ -44,10 +44,11 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", type=int, choices=[2, 3, 4, 5, 6, 7], default=2,
+    ap.add_argument("--config", type=int, choices=[2, 3, 4, 5, 6, 7, 8], default=2,
                     help="2: Llama-3-8B decode (the metric's workload); 3: long-context split-K; "
                          "4: ragged step (cache write + decode); 5: MoE route + dispatch; "
-                         "6: copy_blocks (copy-on-write, 32 layers); 7: swap_blocks out and in")
+                         "6: copy_blocks (copy-on-write, 32 layers); 7: swap_blocks out and in; "
+                         "8: Mixtral MoE MLP (route, dispatch, expert GEMMs, combine)")
     ap.add_argument("--variant", choices=["v1", "v2"], default=None,
                     help="default: v1 for config 2, v2 for configs 3 and 4")
     ap.add_argument("--partition", type=int, default=None,
@@ -86,6 +87,8 @@ def main():
         return bench_moe(args)
     if args.config in (6, 7):
         return bench_blocks(args)
+    if args.config == 8:
+        return bench_moe_mlp(args)
     if args.rotate is None:
         args.rotate = 4
     if args.variant is None:
@@ -353,6 +356,60 @@ def bench_moe(args):
                      "frac": round(value / HBM_PEAK_GBS, 4),
                      "traffic": read_traffic("moe_config5_traffic.json")},
         "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+def bench_moe_mlp(args):
+    """Config 8: the whole Mixtral-8x7B MoE layer after the router: top-2 of
+    8 experts for 4096 tokens (config 5's inputs), the gated expert GEMM
+    (hidden 4096 -> 2 x 14336 with SiLU * up fused), the down GEMM
+    (14336 -> 4096) and the weighted combine. Weights are random fp16, one
+    random matrix per projection copied to every expert on the device."""
+    from swiftllm_amd import _hip, moe, workloads
+    from swiftllm_amd._hip import DeviceArray, Stream
+
+    wl = workloads.moe_config(seed=args.seed)
+    T, hidden = wl.x.shape
+    E, K, I = wl.num_experts, wl.top_k, 14336
+    rng = np.random.default_rng(args.seed + 1)
+    stream = Stream()
+
+    def stacked(n, k):
+        one = (rng.standard_normal((n, k), dtype=np.float32) / np.sqrt(k)).astype(np.float16)
+        d = DeviceArray((E, n, k), np.float16)
+        src = DeviceArray.from_numpy(one)
+        for e in range(E):
+            _hip.check(_hip.hip().hipMemcpy(d.ptr + e * one.nbytes, src.ptr, one.nbytes,
+                                            _hip.HIP_MEMCPY_D2D), "weight copy")
+        src.free()
+        return d
+
+    wg, wu, wd = stacked(I, hidden), stacked(I, hidden), stacked(hidden, I)
+    mlp = moe.MoeMlp(E, K, wg, wu, wd)
+    x, logits = DeviceArray.from_numpy(wl.x), DeviceArray.from_numpy(wl.logits)
+
+    def step(i):
+        mlp.forward(logits, x, stream)
+
+    steps = max(args.steps // 10, 10)
+    warmup = min(args.warmup, 10)
+    ms, p10, p50, p90 = timed(step, stream, steps, warmup, min(args.samples, 20))
+    flops = 2 * T * K * hidden * I * 3
+    tflops = flops / (ms * 1e-3) / 1e12
+    rec = {
+        "metric": "MoE MLP TFLOP/s (expert GEMMs) + us/call @ Mixtral-8x7B layer, 4096 tokens",
+        "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(ms, 6), "us_per_call": round(ms * 1e3, 3),
+        "us_per_call_p10_p50_p90": [round(p10, 2), round(p50, 2), round(p90, 2)],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16 in/out, f32 accumulate", "data": "synthetic (seeded normal activations, logits, weights)",
+        "config": {"workload": "mixtral-8x7b-moe-mlp", "num_tokens": T, "hidden": hidden,
+                   "intermediate": I, "num_experts": E, "top_k": K, "flops_per_call": flops,
+                   "kernels": "rank+route, permute, expert GEMM (gated), expert GEMM, combine"},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(tflops / 2500.0, 4), "traffic": None},
+        "cpu_baseline": None,
     }
     print(json.dumps(rec), flush=True)
 

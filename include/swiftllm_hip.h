@@ -302,6 +302,34 @@ int swiftllm_hip_moe_route_dispatch(const float* logits, const void* x,
                                     hipStream_t stream);
 
 /* ------------------------------------------------------------------------ */
+/* 4b. MoE expert computation: steps 3-4 of MoeMlp::forward                 */
+/*     (crates/swiftllm-models/src/layers/mlp.rs:240-246) over GatedMlp      */
+/*     experts (mlp.rs:118-160: down(silu(gate(x)) * up(x))), Linear weights  */
+/*     [out_features, in_features] (layers/mod.rs:22-24). The reference      */
+/*     returns zeros for all of it.                                           */
+/* ------------------------------------------------------------------------ */
+
+/* Grouped expert GEMM over expert-contiguous rows: expert e owns rows
+ * [expert_offsets[e], expert_offsets[e+1]) of `a` (fp16 [m_total, k], e.g.
+ * the dispatch's x_perm) and of `c` (fp16 [m_total, n]).
+ *   w2 == NULL: c[rows] = a[rows] . w[e]^T
+ *   w2 != NULL: c[rows] = silu(a[rows] . w[e]^T) * (a[rows] . w2[e]^T)
+ * w and w2 are fp16 [E, n, k]. fp32 accumulation. n % 128 == 0 and
+ * k % 64 == 0 are supported (NotSupported otherwise); E <= 256. */
+int swiftllm_hip_moe_expert_gemm(const void* a, const void* w, const void* w2,
+                                 const int32_t* expert_offsets,
+                                 int num_experts, int m_total, int n, int k,
+                                 void* c, hipStream_t stream);
+
+/* out[t, :] = fp16( sum_k weights[t, k] * y[inverse[t, k], :] ), fp32
+ * fused multiply-adds in k order; entries with inverse outside
+ * [0, y_rows) contribute nothing. y fp16 [y_rows, hidden]; hidden % 8 == 0. */
+int swiftllm_hip_moe_combine(const void* y, const float* weights,
+                             const int32_t* inverse, int num_tokens, int top_k,
+                             int hidden, int y_rows, void* out,
+                             hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
 /* 5. Block-table gather check: materialise the K and V of (seq, kv_head) as */
 /*    contiguous [context_len, head_dim] fp16 arrays through the same tile   */
 /*    addressing the decode kernel uses (paged_attention.cu:80-87, 114-116). */

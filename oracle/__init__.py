@@ -19,6 +19,9 @@ reference repository; "cu:" = crates/swiftllm-cuda/kernels/paged_attention.cu):
                              descending order)
   copy_blocks / swap_blocks  numpy: cu:201-227 (launcher cu:302-327) and
                              crates/swiftllm-cuda/src/bindings.rs:200-242
+  silu / moe_expert_gemm /   numpy: MoeMlp steps 3-4 (mlp.rs:240-246) over
+  moe_combine                GatedMlp (mlp.rs:118-160), silu at mlp.rs:263-265,
+                             Linear weights [out, in] (layers/mod.rs:22-24)
 
 Which independent checks pin each function is stated in the tests that use
 it (tests/test_oracle_*.py); every function here has at least one.
@@ -178,6 +181,43 @@ def swap_blocks(src, dst, block_mapping, block_size_bytes: int) -> None:
         if a < 0 or b < 0:
             continue
         d8[b * n:(b + 1) * n] = s8[a * n:(a + 1) * n]
+
+
+def silu(x):
+    """mlp.rs:263-265: x / (1 + exp(-x)), in float64."""
+    x = np.asarray(x, dtype=np.float64)
+    return x / (1.0 + np.exp(-x))
+
+
+def moe_expert_gemm(a, w, w2, offsets):
+    """For each expert e, rows [offsets[e], offsets[e+1]) of a (fp16
+    [m_total, k]) times w[e]^T (Linear layout [n, k]); with w2 the GatedMlp
+    product silu(a.w^T) * (a.w2^T). float64 result [m_total, n]."""
+    a = np.asarray(a, dtype=np.float64)
+    out = np.zeros((a.shape[0], w.shape[1]), np.float64)
+    for e in range(w.shape[0]):
+        r0, r1 = int(offsets[e]), int(offsets[e + 1])
+        if r1 <= r0:
+            continue
+        g = a[r0:r1] @ np.asarray(w[e], dtype=np.float64).T
+        if w2 is not None:
+            g = silu(g) * (a[r0:r1] @ np.asarray(w2[e], dtype=np.float64).T)
+        out[r0:r1] = g
+    return out
+
+
+def moe_combine(y, weights, inverse):
+    """Combine (mlp.rs:245): out[t] = sum_k weights[t, k] * y[inverse[t, k]],
+    entries with inverse < 0 skipped. float64 [T, hidden]."""
+    y = np.asarray(y, dtype=np.float64)
+    inv = np.asarray(inverse)
+    w = np.asarray(weights, dtype=np.float64)
+    T, K = inv.shape
+    out = np.zeros((T, y.shape[1]), np.float64)
+    for k in range(K):
+        ok = inv[:, k] >= 0
+        out[ok] += w[ok, k:k + 1] * y[inv[ok, k]]
+    return out
 
 
 def blocks_needed(num_tokens: int, block_size: int) -> int:

@@ -76,6 +76,8 @@ SIGNATURES = {
         i32, [vp, vp, i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, sz, vp]),
     "swiftllm_hip_moe_route_dispatch": (
         i32, [vp, vp, i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]),
+    "swiftllm_hip_moe_expert_gemm": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp]),
+    "swiftllm_hip_moe_combine": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp]),
     "swiftllm_hip_gather_kv": (
         i32, [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp, vp, vp]),
     "swiftllm_hip_slot_mapping": (i32, [vp, sz, sz, sz, sz, vp]),

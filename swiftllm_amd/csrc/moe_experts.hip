@@ -1,0 +1,364 @@
+// MoE expert computation for gfx950: the grouped expert GEMM (with the
+// SwiGLU gate fused into its epilogue) and the weighted combine.
+//
+// The reference names these steps in MoeMlp::forward
+// (crates/swiftllm-models/src/layers/mlp.rs:240-246: "route tokens to
+// experts", "combine expert outputs") over GatedMlp experts
+// (mlp.rs:118-160: output = down_proj(silu(gate_proj(x)) * up_proj(x)),
+// silu(x) = x / (1 + exp(-x)) at mlp.rs:263-265), with Linear weights laid
+// out [out_features, in_features] (layers/mod.rs:22-24). All of it returns
+// zeros in the reference.
+//
+// expert GEMM: the rows of `a` are expert-contiguous (the dispatch's x_perm:
+//   expert e owns rows [offsets[e], offsets[e+1])). For each expert,
+//   c[rows, :] = a[rows, :] . w[e]^T, or with a second weight (gated)
+//   c = silu(a . w[e]^T) * (a . w2[e]^T). fp16 in, fp32 accumulate, fp16 out.
+//   Workgroup tile 256 activation rows x 256 weight rows (plain: 256 output
+//   columns; gated: 128 gate rows and their 128 up rows), k in steps of 64
+//   staged through double-buffered LDS (147 KiB); eight waves of 128 x 64,
+//   each on v_mfma_f32_32x32x16_f16 with the weight as the MFMA's row
+//   operand, so a lane ends with 4 consecutive output columns of one row
+//   (8-byte stores) and, gated, holds the gate and up value of each of its
+//   columns. The 256 x 256 tile does 128 FLOP per byte staged, so L2 feeds
+//   the matrix cores at ~20 TB/s. Tiles are (expert, 256-row tile, column
+//   tile); a workgroup finds its expert from the offsets, and the grid is
+//   sized for the worst case (ceil(rows / 256) + E row tiles); surplus
+//   workgroups exit at once.
+// combine: out[t, :] = sum_k weights[t, k] * y[inverse[t, k], :] in fp32
+//   (k ascending, fused multiply-add), rounded once to fp16; entries with
+//   inverse -1 contribute nothing.
+
+#include "common.hpp"
+
+namespace swiftllm {
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f16x __attribute__((ext_vector_type(16)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBM = 256;        // activation rows per workgroup tile
+constexpr int kBW = 256;        // weight rows per workgroup tile (gated: 128 gate + 128 up)
+constexpr int kBK = 64;         // k per LDS stage
+constexpr int kPad = 8;         // halfs of padding per LDS row (bank spread)
+constexpr int kLdsRow = kBK + kPad;
+constexpr int kThreads = 512;   // 8 waves: 2 (rows) x 4 (weight rows), 128 x 64 each
+constexpr int kChunks = kBM * kBK / 8 / kThreads;  // 16-byte loads per thread per tile
+constexpr int kMaxE = 256;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kXcds = 8;                 // MI355X: 8 XCDs, each with its own L2
+constexpr int kSuperM = 4;               // row tiles per super-tile
+constexpr int kSuperN = 8;               // column tiles per super-tile
+constexpr int kSuper = kSuperM * kSuperN;
+
+struct GemmArgs {
+    const f16* a;        // [m_total][k]
+    const f16* w;        // [E][n][k]
+    const f16* w2;       // [E][n][k] or null
+    const int* offsets;  // [E + 1]
+    f16* c;              // [m_total][n]
+    int E;
+    int m_total;
+    int n;
+    int k;
+    int m_tiles_max;     // row tiles the grid covers
+    int n_tiles;         // column tiles
+    int sm;              // super-tiles along the rows
+};
+
+__device__ __forceinline__ f16x mfma32(h8 a, h8 b, f16x c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Output columns per workgroup tile: 256 plain, 128 gated (each column needs
+// its gate and its up row).
+template <bool GATED>
+constexpr int tile_cols() { return GATED ? kBW / 2 : kBW; }
+
+template <bool GATED>
+__global__ __launch_bounds__(kThreads) void moe_expert_gemm_kernel(const GemmArgs a) {
+    extern __shared__ __align__(16) f16 lds[];
+    __shared__ int s_tile0[kMaxE + 1];  // first global row tile of each expert
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wv = tid >> 6;
+
+    // Which (row tile, column tile). Workgroups go to the 8 XCDs round
+    // robin, so slot = blockIdx / 8 is the order within one XCD. Each XCD
+    // takes super-tiles of 4 row tiles x 8 column tiles in turn: its 32
+    // resident workgroups then share every activation k-tile 8 ways and
+    // every weight k-tile 4 ways in that XCD's L2. Row tiles enumerate
+    // (expert, tile) in expert order.
+    const int xcd = blockIdx.x & (kXcds - 1);
+    const int slot = blockIdx.x / kXcds;
+    const int st = (slot / kSuper) * kXcds + xcd;     // super-tile
+    const int idx = slot % kSuper;
+    const int sm = st % a.sm;
+    const int mt = sm * kSuperM + idx % kSuperM;
+    const int nt = (st / a.sm) * kSuperN + idx / kSuperM;
+    if (tid < 64) {
+        int run = 0;
+        for (int e0 = 0; e0 < a.E; e0 += 64) {
+            const int e = e0 + lane;
+            int v = 0;
+            if (e < a.E) v = max(a.offsets[e + 1] - a.offsets[e], 0);
+            v = (v + kBM - 1) / kBM;
+            int x = v;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const int y = __shfl_up(x, d);
+                if (lane >= d) x += y;
+            }
+            if (e < a.E) s_tile0[e] = run + x - v;
+            run += __shfl(x, 63);
+        }
+        if (lane == 0) s_tile0[a.E] = run;
+    }
+    __syncthreads();
+    if (mt >= s_tile0[a.E] || nt >= a.n_tiles) return;
+    int lo = 0, hi = a.E;  // s_tile0[lo] <= mt < s_tile0[hi]
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (s_tile0[mid] <= mt) lo = mid; else hi = mid;
+    }
+    const int e = lo;
+    const int row0 = a.offsets[e] + (mt - s_tile0[e]) * kBM;
+    const int row_end = min(a.offsets[e + 1], a.m_total);  // rows past m_total are never touched
+    if (row0 < 0 || row0 >= row_end) return;
+    const int col0 = nt * tile_cols<GATED>();
+
+    f16* lx = lds;                       // [2][kBM][kLdsRow]
+    f16* lw = lds + 2 * kBM * kLdsRow;   // [2][kBW][kLdsRow]
+    const size_t K = static_cast<size_t>(a.k);
+    const f16* wbase = a.w + (static_cast<size_t>(e) * a.n + col0) * K;
+    const f16* w2base = GATED ? a.w2 + (static_cast<size_t>(e) * a.n + col0) * K : nullptr;
+
+    // Loader: thread tid moves 16-byte chunks c = tid + 512 j of each tile
+    // (row c / 8, k chunk c % 8). Rows past the expert repeat its last row.
+    // Gated: weight rows 0..127 of the tile are gate rows, 128..255 up rows.
+    u32x4 rx[kChunks], rw[kChunks];
+    auto load_stage = [&](int k0) {
+#pragma unroll
+        for (int j = 0; j < kChunks; ++j) {
+            const int c = tid + kThreads * j;
+            const int r = c >> 3, kc = (c & 7) * 8;
+            const int row = min(row0 + r, row_end - 1);
+            rx[j] = *reinterpret_cast<const u32x4*>(a.a + static_cast<size_t>(row) * K + k0 + kc);
+            const f16* wr = (GATED && r >= kBW / 2) ? w2base + static_cast<size_t>(r - kBW / 2) * K
+                                                    : wbase + static_cast<size_t>(r) * K;
+            rw[j] = *reinterpret_cast<const u32x4*>(wr + k0 + kc);
+        }
+    };
+    auto store_stage = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < kChunks; ++j) {
+            const int c = tid + kThreads * j;
+            const int r = c >> 3, kc = (c & 7) * 8;
+            *reinterpret_cast<u32x4*>(lx + (buf * kBM + r) * kLdsRow + kc) = rx[j];
+            *reinterpret_cast<u32x4*>(lw + (buf * kBW + r) * kLdsRow + kc) = rw[j];
+        }
+    };
+
+    // Wave (wm, wn): activation rows wm*128 .. +128 as 4 MFMA column tiles
+    // (j) and two 32-row weight tiles (i) at LDS weight row wrow(i):
+    // plain: wn*64 + 32 i (output columns wn*64 + 32 i ..);
+    // gated: i = 0 gate rows wn*32 .., i = 1 the matching up rows.
+    const int wm = wv & 1, wn = wv >> 1;
+    auto wrow = [&](int i) { return GATED ? i * (kBW / 2) + wn * 32 : wn * 64 + i * 32; };
+    f16x acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f16x{};
+
+    const int nk = a.k / kBK;
+    load_stage(0);
+    store_stage(0);
+    __syncthreads();
+    const int lr = lane & 31;          // MFMA row / column within a 32 tile
+    const int lk = (lane >> 5) * 8;    // k offset of this lane's 8 values
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) load_stage((kt + 1) * kBK);
+        const f16* bx = lx + buf * kBM * kLdsRow;
+        const f16* bw = lw + buf * kBW * kLdsRow;
+#pragma unroll
+        for (int ks = 0; ks < kBK; ks += 16) {
+            h8 xo[4], wo[2];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                xo[j] = *reinterpret_cast<const h8*>(bx + (wm * 128 + j * 32 + lr) * kLdsRow + ks + lk);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                wo[i] = *reinterpret_cast<const h8*>(bw + (wrow(i) + lr) * kLdsRow + ks + lk);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = mfma32(wo[i], xo[j], acc[i][j]);
+        }
+        if (kt + 1 < nk) store_stage(buf ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue: lane holds output row (tile j) lr and, per weight tile i,
+    // columns q*8 + (lane/32)*4 + 0..3, q = 0..3.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int row = row0 + wm * 128 + j * 32 + lr;
+        if (row >= row_end) continue;
+        f16* crow = a.c + static_cast<size_t>(row) * a.n + col0;
+#pragma unroll
+        for (int i = 0; i < (GATED ? 1 : 2); ++i) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                h4 v;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float x = acc[i][j][q * 4 + r];
+                    if (GATED) {
+                        const float u = acc[1][j][q * 4 + r];
+                        x = x / (1.0f + __builtin_amdgcn_exp2f(-x * kLog2e)) * u;
+                    }
+                    v[r] = static_cast<f16>(x);
+                }
+                const int col = (GATED ? wn * 32 : wn * 64 + i * 32) + q * 8 + (lane >> 5) * 4;
+                *reinterpret_cast<h4*>(crow + col) = v;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Combine: one wave per token, 8 halfs per lane per step.
+// ---------------------------------------------------------------------------
+struct CombineArgs {
+    const f16* y;        // [T*K][hidden]
+    const float* wts;    // [T][K]
+    const int* inverse;  // [T][K]
+    f16* out;            // [T][hidden]
+    int T;
+    int K;
+    int hidden;
+    int rows;            // rows of y (bound on inverse)
+};
+
+__global__ __launch_bounds__(256) void moe_combine_kernel(const CombineArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= a.T) return;
+    const int nv = a.hidden / 8;
+    for (int i = lane; i < nv; i += 64) {
+        float acc[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) acc[r] = 0.0f;
+        for (int k = 0; k < a.K; ++k) {
+            const int row = a.inverse[static_cast<size_t>(t) * a.K + k];
+            if (row < 0 || row >= a.rows) continue;
+            const float w = a.wts[static_cast<size_t>(t) * a.K + k];
+            const h8 v = *reinterpret_cast<const h8*>(a.y + static_cast<size_t>(row) * a.hidden + 8 * i);
+#pragma unroll
+            for (int r = 0; r < 8; ++r) acc[r] = __builtin_fmaf(w, static_cast<float>(v[r]), acc[r]);
+        }
+        h8 o;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) o[r] = static_cast<f16>(acc[r]);
+        *reinterpret_cast<h8*>(a.out + static_cast<size_t>(t) * a.hidden + 8 * i) = o;
+    }
+}
+
+}  // namespace
+}  // namespace swiftllm
+
+using namespace swiftllm;
+
+extern "C" {
+
+int swiftllm_hip_moe_expert_gemm(const void* a, const void* w, const void* w2,
+                                 const int32_t* expert_offsets, int num_experts, int m_total,
+                                 int n, int k, void* c, hipStream_t stream) {
+    const char* who = "swiftllm_hip_moe_expert_gemm";
+    if (num_experts <= 0 || m_total < 0 || n <= 0 || k <= 0) {
+        return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: num_experts=%d m_total=%d n=%d k=%d", who,
+                    num_experts, m_total, n, k);
+    }
+    const int cols = (w2 != nullptr) ? tile_cols<true>() : tile_cols<false>();
+    if (num_experts > kMaxE || n % cols != 0 || k % kBK != 0) {
+        return fail(SWIFTLLM_ERR_NOT_SUPPORTED,
+                    "%s: num_experts=%d n=%d k=%d (supported: E <= 256, n a multiple of %d, k of 64)",
+                    who, num_experts, n, k, cols);
+    }
+    if (!w || !expert_offsets || (m_total > 0 && (!a || !c))) {
+        return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: null pointer", who);
+    }
+    if (!aligned(a, 16) || !aligned(w, 16) || !aligned(w2, 16) || !aligned(c, 8) ||
+        !aligned(expert_offsets, 4)) {
+        return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: misaligned pointer", who);
+    }
+    int rc = require_device();
+    if (rc != SWIFTLLM_OK) return rc;
+    if (m_total == 0) return ok();
+    GemmArgs g{};
+    g.a = static_cast<const f16*>(a);
+    g.w = static_cast<const f16*>(w);
+    g.w2 = static_cast<const f16*>(w2);
+    g.offsets = expert_offsets;
+    g.c = static_cast<f16*>(c);
+    g.E = num_experts;
+    g.m_total = m_total;
+    g.n = n;
+    g.k = k;
+    g.m_tiles_max = (m_total + kBM - 1) / kBM + num_experts;
+    g.n_tiles = n / cols;
+    g.sm = (g.m_tiles_max + kSuperM - 1) / kSuperM;
+    const long long supers = static_cast<long long>(g.sm) * ((g.n_tiles + kSuperN - 1) / kSuperN);
+    // whole rounds of 8 super-tiles, one per XCD
+    const long long grid = (supers + kXcds - 1) / kXcds * kXcds * kSuper;
+    if (grid > 0x7fffffffLL) {
+        return fail(SWIFTLLM_ERR_NOT_SUPPORTED, "%s: %lld tiles", who, grid);
+    }
+    // Dynamic LDS: two stages of the activation and weight tiles (147 KiB),
+    // above the default limit, so the limit is raised.
+    const bool gated = (w2 != nullptr);
+    const size_t lds = 2 * (kBM + kBW) * kLdsRow * sizeof(f16);
+    const void* fn = gated ? reinterpret_cast<const void*>(moe_expert_gemm_kernel<true>)
+                           : reinterpret_cast<const void*>(moe_expert_gemm_kernel<false>);
+    hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         static_cast<int>(lds));
+    if (err != hipSuccess) return launched(err, who);
+    err = gated ? launch(moe_expert_gemm_kernel<true>, dim3(static_cast<unsigned>(grid)),
+                         dim3(kThreads), lds, stream, g)
+                : launch(moe_expert_gemm_kernel<false>, dim3(static_cast<unsigned>(grid)),
+                         dim3(kThreads), lds, stream, g);
+    return launched(err, who);
+}
+
+int swiftllm_hip_moe_combine(const void* y, const float* weights, const int32_t* inverse,
+                             int num_tokens, int top_k, int hidden, int y_rows, void* out,
+                             hipStream_t stream) {
+    const char* who = "swiftllm_hip_moe_combine";
+    if (num_tokens < 0 || top_k <= 0 || hidden <= 0 || y_rows < 0) {
+        return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: num_tokens=%d top_k=%d hidden=%d y_rows=%d",
+                    who, num_tokens, top_k, hidden, y_rows);
+    }
+    if (hidden % 8 != 0) {
+        return fail(SWIFTLLM_ERR_NOT_SUPPORTED, "%s: hidden=%d (a multiple of 8 is supported)", who,
+                    hidden);
+    }
+    if (num_tokens > 0 && (!y || !weights || !inverse || !out)) {
+        return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: null pointer", who);
+    }
+    if (!aligned(y, 16) || !aligned(out, 16) || !aligned(weights, 4) || !aligned(inverse, 4)) {
+        return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: misaligned pointer", who);
+    }
+    int rc = require_device();
+    if (rc != SWIFTLLM_OK) return rc;
+    if (num_tokens == 0) return ok();
+    CombineArgs g{static_cast<const f16*>(y), weights, inverse, static_cast<f16*>(out), num_tokens,
+                  top_k, hidden, y_rows};
+    return launched(launch(moe_combine_kernel, dim3((num_tokens + 3) / 4), dim3(256), 0, stream, g),
+                    who);
+}
+
+}  // extern "C"

@@ -84,6 +84,72 @@ def moe_route_dispatch(logits: DeviceArray, x: Optional[DeviceArray], top_k: int
         stream.handle if stream else None))
 
 
+def moe_expert_gemm(a: DeviceArray, w: DeviceArray, w2: Optional[DeviceArray],
+                    expert_offsets: DeviceArray, c: DeviceArray,
+                    stream: Optional[Stream] = None) -> None:
+    """Grouped expert GEMM over expert-contiguous rows: a fp16 [m_total, k],
+    w (and w2) fp16 [E, n, k], c fp16 [m_total, n]; with w2 the SwiGLU
+    product silu(a.w^T) * (a.w2^T)."""
+    m_total, k = a.shape
+    E, n, kw = w.shape
+    if kw != k or c.shape != (m_total, n) or (w2 is not None and w2.shape != w.shape):
+        raise ValueError(f"shapes a{a.shape} w{w.shape} c{c.shape}")
+    check_status(_lib.lib().swiftllm_hip_moe_expert_gemm(
+        a.ptr, w.ptr, w2.ptr if w2 is not None else None, expert_offsets.ptr, E, m_total, n, k,
+        c.ptr, stream.handle if stream else None))
+
+
+def moe_combine(y: DeviceArray, weights: DeviceArray, inverse: DeviceArray, out: DeviceArray,
+                stream: Optional[Stream] = None) -> None:
+    """out[t] = sum_k weights[t, k] * y[inverse[t, k]] (fp32, then fp16)."""
+    T, K = inverse.shape
+    rows, hidden = y.shape
+    check_status(_lib.lib().swiftllm_hip_moe_combine(
+        y.ptr, weights.ptr, inverse.ptr, T, K, hidden, rows, out.ptr,
+        stream.handle if stream else None))
+
+
+class MoeMlp:
+    """MoeMlp::forward (mlp.rs:207-252) from router logits on: top-k
+    routing, dispatch, the gated expert GEMM (GatedMlp, mlp.rs:118-160), the
+    down-projection GEMM and the weighted combine. Expert weights are stacked
+    fp16 device arrays: gate_proj and up_proj [E, I, hidden], down_proj
+    [E, hidden, I]."""
+
+    def __init__(self, num_experts: int, num_experts_per_tok: int, gate_proj: DeviceArray,
+                 up_proj: DeviceArray, down_proj: DeviceArray):
+        self.num_experts = num_experts
+        self.num_experts_per_tok = num_experts_per_tok
+        self.gate_proj, self.up_proj, self.down_proj = gate_proj, up_proj, down_proj
+        self.intermediate = gate_proj.shape[1]
+        self._bufs = {}
+
+    def buffers(self, T: int, hidden: int):
+        key = (T, hidden)
+        if key not in self._bufs:
+            K, I = self.num_experts_per_tok, self.intermediate
+            self._bufs[key] = dict(
+                ids=DeviceArray((T, K), np.int32), weights=DeviceArray((T, K), np.float32),
+                dispatch=DispatchBuffers.allocate(T, self.num_experts, K, hidden),
+                h=DeviceArray((max(T * K, 1), I), np.float16),
+                y=DeviceArray((max(T * K, 1), hidden), np.float16),
+                out=DeviceArray((T, hidden), np.float16))
+        return self._bufs[key]
+
+    def forward(self, router_logits: DeviceArray, x: DeviceArray,
+                stream: Optional[Stream] = None) -> DeviceArray:
+        T, hidden = x.shape
+        b = self.buffers(T, hidden)
+        d = b["dispatch"]
+        moe_route_dispatch(router_logits, x, self.num_experts_per_tok, b["ids"], b["weights"], d,
+                           stream)
+        if T > 0:
+            moe_expert_gemm(d.x_perm, self.gate_proj, self.up_proj, d.offsets, b["h"], stream)
+            moe_expert_gemm(b["h"], self.down_proj, None, d.offsets, b["y"], stream)
+        moe_combine(b["y"], b["weights"], d.inverse, b["out"], stream)
+        return b["out"]
+
+
 class MoeRouting:
     """The routing half of MoeMlp (mlp.rs:209-221 fields num_experts,
     num_experts_per_tok): route(logits) then dispatch(x)."""

@@ -1,0 +1,108 @@
+"""MoE expert computation on the GPU against the float64 oracle: the grouped
+expert GEMM (plain and with the fused SwiGLU gate), the weighted combine,
+and the whole MoeMlp chain (route, dispatch, gated GEMM, down GEMM,
+combine) at a small Mixtral-like shape.
+
+Tolerance: fp16 outputs of fp32 accumulation against float64 on the same
+fp16 inputs: |gpu - ref| <= 2^-10 |ref| + 1e-3 rms(ref) (one fp16 rounding
+plus fp32 accumulation; an indexing mistake is off by O(rms)). The combine is
+held to one fp16 ulp."""
+
+import numpy as np
+import pytest
+
+import oracle
+from swiftllm_amd import moe
+from swiftllm_amd._hip import DeviceArray, synchronize
+
+pytestmark = pytest.mark.gpu
+
+
+def _close(gpu, ref, what):
+    gpu = np.asarray(gpu, np.float64)
+    assert np.all(np.isfinite(gpu)), what
+    rms = float(np.sqrt(np.mean(ref ** 2))) if ref.size else 0.0
+    err = np.abs(gpu - ref)
+    bound = 2.0 ** -10 * np.abs(ref) + 1e-3 * rms
+    worst = float((err - bound).max()) if err.size else -1.0
+    assert worst <= 0, f"{what}: max err {err.max():.3e}, rms {rms:.3e}"
+
+
+def _offsets(rng, E, m_total, empty=()):
+    cuts = np.sort(rng.integers(0, m_total + 1, size=E - 1))
+    counts = np.diff(np.concatenate([[0], cuts, [m_total]]))
+    for e in empty:  # move an expert's rows to the next one
+        counts[(e + 1) % E] += counts[e]
+        counts[e] = 0
+    return np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+
+
+@pytest.mark.parametrize("gated", [False, True])
+@pytest.mark.parametrize("E,m_total,n,k", [
+    (4, 300, 256, 128),
+    (8, 1000, 512, 192),
+    (1, 257, 256, 64),       # one expert, a 1-row tail tile
+    (3, 0, 256, 64),
+])
+def test_expert_gemm(dev, gated, E, m_total, n, k):
+    """Tiles of 256 rows; columns in tiles of 256 (plain) or 128 (gated)."""
+    rng = np.random.default_rng(E * 1000 + m_total + gated)
+    offs = _offsets(rng, E, m_total, empty=(1,) if E > 2 else ())
+    a = (rng.standard_normal((max(m_total, 1), k)) * 0.5).astype(np.float16)[:m_total]
+    w = (rng.standard_normal((E, n, k)) / np.sqrt(k)).astype(np.float16)
+    w2 = (rng.standard_normal((E, n, k)) / np.sqrt(k)).astype(np.float16) if gated else None
+    ad = DeviceArray.from_numpy(a) if m_total else DeviceArray((0, k), np.float16)
+    c = DeviceArray((m_total, n), np.float16)
+    c.fill_byte(0xFF)
+    moe.moe_expert_gemm(ad, DeviceArray.from_numpy(w),
+                        DeviceArray.from_numpy(w2) if gated else None,
+                        DeviceArray.from_numpy(offs), c)
+    synchronize()
+    if m_total:
+        _close(c.numpy().astype(np.float64), oracle.moe_expert_gemm(a, w, w2, offs),
+               f"gemm gated={gated} E{E} M{m_total}")
+
+
+def test_combine_one_ulp(dev):
+    rng = np.random.default_rng(21)
+    T, K, hidden = 500, 2, 4096
+    y = rng.standard_normal((T * K, hidden)).astype(np.float16)
+    wts = rng.random((T, K)).astype(np.float32)
+    inv = rng.permutation(T * K).reshape(T, K).astype(np.int32)
+    inv[::13, 1] = -1
+    out = DeviceArray((T, hidden), np.float16)
+    moe.moe_combine(DeviceArray.from_numpy(y), DeviceArray.from_numpy(wts),
+                    DeviceArray.from_numpy(inv), out)
+    synchronize()
+    got = out.numpy()
+    ref = oracle.moe_combine(y, wts, inv).astype(np.float16)
+    # adjacent fp16 values differ by 1 in their ordered bit patterns
+    def ordered(h):
+        b = h.view(np.int16).astype(np.int32)
+        return np.where(b < 0, -32768 - b, b)
+    assert np.abs(ordered(got) - ordered(ref)).max() <= 1
+    assert np.mean(got.view(np.uint16) == ref.view(np.uint16)) > 0.99
+
+
+def test_moe_mlp_chain(dev):
+    """MoeMlp from router logits: top-2 of 8 experts, hidden 256,
+    intermediate 512, against the oracle chain with the same fp16 rounding
+    of the intermediate activations."""
+    rng = np.random.default_rng(22)
+    T, hidden, I, E, K = 96, 256, 512, 8, 2
+    x = rng.standard_normal((T, hidden)).astype(np.float16)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    wg = (rng.standard_normal((E, I, hidden)) / np.sqrt(hidden)).astype(np.float16)
+    wu = (rng.standard_normal((E, I, hidden)) / np.sqrt(hidden)).astype(np.float16)
+    wd = (rng.standard_normal((E, hidden, I)) / np.sqrt(I)).astype(np.float16)
+    mlp = moe.MoeMlp(E, K, DeviceArray.from_numpy(wg), DeviceArray.from_numpy(wu),
+                     DeviceArray.from_numpy(wd))
+    out = mlp.forward(DeviceArray.from_numpy(logits), DeviceArray.from_numpy(x))
+    synchronize()
+    ids, w = oracle.moe_route(logits, K)
+    counts, offsets, inverse, sorted_ids = oracle.moe_dispatch(ids, E)
+    xp = x[sorted_ids]
+    h = oracle.moe_expert_gemm(xp, wg, wu, offsets).astype(np.float16)
+    y = oracle.moe_expert_gemm(h, wd, None, offsets).astype(np.float16)
+    ref = oracle.moe_combine(y, w.astype(np.float32), inverse)
+    _close(out.numpy().astype(np.float64), ref, "moe mlp")

@@ -218,3 +218,64 @@ def test_swap_blocks_matches_byte_loop():
                 expect[b * nbytes + i] = src[a * nbytes + i]
     oracle.swap_blocks(src, dst, mapping, nbytes)
     assert np.array_equal(dst, expect)
+
+
+def test_silu_reference_kats_and_identities():
+    """mlp.rs:313-317 (test_activation_silu): silu(0) = 0, silu(1) > 0.7,
+    silu(-1) < -0.2; and silu(x) - silu(-x) = x, silu(x) = x * sigmoid(x)."""
+    assert abs(oracle.silu(0.0)) < 1e-6
+    assert oracle.silu(1.0) > 0.7
+    assert oracle.silu(-1.0) < -0.2
+    x = np.linspace(-20, 20, 81)
+    assert np.allclose(oracle.silu(x) - oracle.silu(-x), x, atol=1e-12)
+    assert np.allclose(oracle.silu(x), x * (0.5 * (1 + np.tanh(x / 2))), atol=1e-12)
+
+
+def _expert_gemm_brute(a, w, w2, offsets):
+    m, n = a.shape[0], w.shape[1]
+    out = np.zeros((m, n))
+    for e in range(w.shape[0]):
+        for r in range(int(offsets[e]), int(offsets[e + 1])):
+            for j in range(n):
+                g = sum(float(a[r, q]) * float(w[e, j, q]) for q in range(a.shape[1]))
+                if w2 is not None:
+                    u = sum(float(a[r, q]) * float(w2[e, j, q]) for q in range(a.shape[1]))
+                    g = g / (1 + math.exp(-g)) * u
+                out[r, j] = g
+    return out
+
+
+@pytest.mark.parametrize("gated", [False, True])
+def test_expert_gemm_matches_brute_force(gated):
+    rng = np.random.default_rng(11 + gated)
+    E, n, k = 3, 5, 7
+    offsets = np.array([0, 4, 4, 9], np.int32)          # expert 1 has no rows
+    a = rng.standard_normal((9, k)).astype(np.float16)
+    w = rng.standard_normal((E, n, k)).astype(np.float16)
+    w2 = rng.standard_normal((E, n, k)).astype(np.float16) if gated else None
+    got = oracle.moe_expert_gemm(a, w, w2, offsets)
+    assert np.allclose(got, _expert_gemm_brute(a, w, w2, offsets), atol=1e-12)
+
+
+def test_planted_expert_off_by_one_is_caught():
+    rng = np.random.default_rng(12)
+    offsets = np.array([0, 3, 6], np.int32)
+    a = rng.standard_normal((6, 4)).astype(np.float16)
+    w = rng.standard_normal((2, 3, 4)).astype(np.float16)
+    good = oracle.moe_expert_gemm(a, w, None, offsets)
+    planted = oracle.moe_expert_gemm(a, w, None, np.array([0, 4, 6], np.int32))
+    assert not np.allclose(good, planted)
+
+
+def test_combine_matches_brute_force():
+    rng = np.random.default_rng(13)
+    T, K, hidden = 6, 3, 5
+    y = rng.standard_normal((T * K, hidden)).astype(np.float16)
+    w = rng.random((T, K)).astype(np.float32)
+    inv = rng.permutation(T * K).reshape(T, K).astype(np.int32)
+    inv[2, 1] = -1
+    got = oracle.moe_combine(y, w, inv)
+    for t in range(T):
+        for d in range(hidden):
+            ref = sum(float(w[t, k]) * float(y[inv[t, k], d]) for k in range(K) if inv[t, k] >= 0)
+            assert abs(got[t, d] - ref) < 1e-12
