@@ -44,11 +44,12 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", type=int, choices=[2, 3, 4, 5, 6, 7, 8], default=2,
+    ap.add_argument("--config", type=int, choices=[2, 3, 4, 5, 6, 7, 8, 9], default=2,
                     help="2: Llama-3-8B decode (the metric's workload); 3: long-context split-K; "
                          "4: ragged step (cache write + decode); 5: MoE route + dispatch; "
                          "6: copy_blocks (copy-on-write, 32 layers); 7: swap_blocks out and in; "
-                         "8: Mixtral MoE MLP (route, dispatch, expert GEMMs, combine)")
+                         "8: Mixtral MoE MLP (route, dispatch, expert GEMMs, combine); "
+                         "9: Llama-3-8B paged prefill (8 prompts of 2048 tokens)")
     ap.add_argument("--variant", choices=["v1", "v2"], default=None,
                     help="default: v1 for config 2, v2 for configs 3 and 4")
     ap.add_argument("--partition", type=int, default=None,
@@ -89,6 +90,8 @@ def main():
         return bench_blocks(args)
     if args.config == 8:
         return bench_moe_mlp(args)
+    if args.config == 9:
+        return bench_prefill(args)
     if args.rotate is None:
         args.rotate = 4
     if args.variant is None:
@@ -356,6 +359,49 @@ def bench_moe(args):
                      "frac": round(value / HBM_PEAK_GBS, 4),
                      "traffic": read_traffic("moe_config5_traffic.json")},
         "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+def bench_prefill(args):
+    """Config 9: paged prefill at the Llama-3-8B layer shape (32 query heads,
+    8 kv heads, head_dim 128): 8 prompts of 2048 tokens packed (16384
+    tokens), their K/V already in a randomly permuted block pool. A step is
+    one causal-attention call over the batch."""
+    from swiftllm_amd import paged_attention as pa
+    from swiftllm_amd import workloads
+    from swiftllm_amd._hip import DeviceArray, Stream
+
+    w = workloads.prefill_config((2048,) * 8, 32, 8, 128, seed=args.seed, poison=False)
+    T, H, D = w.q.shape
+    S = len(w.context_lens)
+    stream = Stream()
+    q = DeviceArray.from_numpy(w.q)
+    kc, vc = DeviceArray.from_numpy(w.key_cache), DeviceArray.from_numpy(w.value_cache)
+    sm, ctx = DeviceArray.from_numpy(w.slot_mapping), DeviceArray.from_numpy(w.context_lens)
+    out = DeviceArray((T, H, D), np.float16)
+
+    def step(i):
+        pa.launch_paged_prefill(out, q, kc, vc, sm, ctx, w.scale, S, H, 8, D, 16, 2048,
+                                num_blocks=w.key_cache.shape[0], stream=stream)
+
+    steps = max(args.steps // 10, 10)
+    warmup = min(args.warmup, 10)
+    ms, p10, p50, p90 = timed(step, stream, steps, warmup, min(args.samples, 50))
+    tflops = w.flops() / (ms * 1e-3) / 1e12
+    rec = {
+        "metric": "paged prefill TFLOP/s (causal attention) + us/call @ Llama-3-8B layer, 8 x 2048 tokens",
+        "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(ms, 6), "us_per_call": round(ms * 1e3, 3),
+        "us_per_call_p10_p50_p90": [round(p10, 2), round(p50, 2), round(p90, 2)],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16 in/out, f32 accumulate", "data": "synthetic (seeded normal fp16 Q/K/V)",
+        "config": {"workload": "llama3-8b-prefill-layer", "prompts": S, "prompt_len": 2048,
+                   "num_heads": H, "num_kv_heads": 8, "head_dim": D, "block_size": 16,
+                   "flops_per_call": w.flops(), "algorithmic_bytes_per_call": w.bytes()},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(tflops / 2500.0, 4), "traffic": None},
+        "cpu_baseline": None,
     }
     print(json.dumps(rec), flush=True)
 

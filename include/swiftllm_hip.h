@@ -138,7 +138,8 @@ int swiftllm_hip_workspace_clear(void* workspace, size_t bytes,
 /* 2. Status-returning twins of the launchers (same arguments; return a     */
 /*    swiftllm_status). num_blocks bounds every block id read from           */
 /*    block_tables / slot_mapping: ids outside [0, num_blocks) are skipped.  */
-/*    Pass num_blocks <= 0 when the pool size is unknown (no bound).         */
+/*    Pass num_blocks <= 0 when the pool size is unknown (no bound);         */
+/*    negative ids are skipped in either case.                               */
 /* ------------------------------------------------------------------------ */
 int swiftllm_hip_launch_paged_attention_v1(
     void* output, const void* query, const void* key_cache,
@@ -198,6 +199,37 @@ int swiftllm_hip_reshape_and_cache(const void* key, const void* value,
                                    const int32_t* slot_mapping,
                                    const swiftllm_reshape_cache_params* params,
                                    hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* 3a. Paged prefill (causal attention over a packed batch of prompts).      */
+/* ------------------------------------------------------------------------ */
+
+/* Replaces bindings::paged_attention_prefill (bindings.rs:32-54): the steps
+ * of PagedAttention::prefill (paged_attention.rs:154-189) after the K/V
+ * write. query / output fp16 [T, H, D] packed: sequence s owns tokens
+ * [start_s, start_s + context_lens[s]), start_s the sum of the lengths
+ * before it. Token i of s attends to tokens j <= i of s, whose K/V sit in
+ * the cache at slot_mapping[start_s + j]; the slots of a sequence must walk
+ * its block table from position 0 (table[p / 16] * 16 + p % 16).
+ * params->max_context_len bounds every context_lens[s]. */
+int swiftllm_hip_paged_attention_prefill(
+    void* output, const void* query, const void* key_cache,
+    const void* value_cache, const int32_t* slot_mapping,
+    const int32_t* context_lens, const swiftllm_paged_attention_params* params,
+    hipStream_t stream);
+
+/* The same with plain arguments and a pool bound: blocks outside
+ * [0, num_blocks) are skipped (num_blocks <= 0: no bound; negative block ids
+ * are always skipped). */
+int swiftllm_hip_launch_paged_prefill(void* output, const void* query,
+                                      const void* key_cache,
+                                      const void* value_cache,
+                                      const int32_t* slot_mapping,
+                                      const int32_t* context_lens, float scale,
+                                      int num_seqs, int num_heads,
+                                      int num_kv_heads, int head_dim,
+                                      int block_size, int max_context_len,
+                                      int num_blocks, hipStream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* 3b. Block copies of the KV cache. block_mapping holds num_pairs (src, dst) */

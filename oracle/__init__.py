@@ -10,6 +10,9 @@ reference repository; "cu:" = crates/swiftllm-cuda/kernels/paged_attention.cu):
   decode_f64 / decode_f32    C (liboracle.so): cu:35-137 contract, textbook
                              softmax attention, fp64 resp. fp32 accumulation
   decode_numpy               numpy fp64 restatement of the same (small cases)
+  prefill_numpy              numpy fp64: causal attention over packed prompts
+                             whose K/V sit at slot_mapping (bindings.rs:32-54,
+                             paged_attention.rs:154-189)
   reshape_and_cache          C and numpy: cu:167-199
   gather_kv                  numpy: cu:80-87, 114-116 block-table gather
   slot_mapping               kv_cache.rs:186-216 (crates/swiftllm-core/src/memory)
@@ -135,6 +138,37 @@ def decode_numpy(q, kc, vc, bt, ctx, scale, kv_head_of=None) -> np.ndarray:
             logit = (K[kvh] @ q[s, h].astype(np.float64)) * scale
             p = np.exp(logit - logit.max())
             out[s, h] = (p @ V[kvh]) / p.sum()
+    return out
+
+
+def prefill_numpy(q, kc, vc, slot_mapping, context_lens, scale) -> np.ndarray:
+    """Steps 1-4 of paged_attention.rs:154-189 in float64: sequence s owns
+    the packed tokens [start_s, start_s + L_s); token i attends to tokens
+    j <= i of its sequence, whose K/V are read at slot_mapping (cache element
+    (slot // BS, kvh, d, slot % BS), cu:80-87 addressing); kvh = h // (H / Hkv)."""
+    T, H, D = q.shape
+    BS = kc.shape[3]
+    Hkv = kc.shape[1]
+    G = H // Hkv
+    out = np.zeros((T, H, D), np.float64)
+    start = 0
+    for L in np.maximum(np.asarray(context_lens, dtype=np.int64), 0):
+        L = int(L)
+        if L:
+            sl = np.asarray(slot_mapping[start:start + L], dtype=np.int64)
+            b, o = sl // BS, sl % BS
+            K = kc[b, :, :, o].astype(np.float64)   # [L, Hkv, D]
+            V = vc[b, :, :, o].astype(np.float64)
+            mask = np.tril(np.ones((L, L), bool))
+            for h in range(H):
+                qh = q[start:start + L, h].astype(np.float64)
+                sc = (qh @ K[:, h // G].T) * scale
+                sc = np.where(mask, sc, -np.inf)
+                sc -= sc.max(axis=1, keepdims=True)
+                p = np.exp(sc)
+                p /= p.sum(axis=1, keepdims=True)
+                out[start:start + L, h] = p @ V[:, h // G]
+        start += L
     return out
 
 

@@ -67,6 +67,9 @@ SIGNATURES = {
         i32, [vp, vp, vp, vp, vp, ctypes.POINTER(ReshapeCacheParams), vp]),
     "swiftllm_hip_moe_route": (i32, [vp, i32, i32, i32, vp, vp, vp]),
     "swiftllm_hip_moe_dispatch_workspace_size": (sz, [i32, i32, i32]),
+    "swiftllm_hip_paged_attention_prefill": (i32, [vp, vp, vp, vp, vp, vp, vp, vp]),
+    "swiftllm_hip_launch_paged_prefill": (
+        i32, [vp, vp, vp, vp, vp, vp, f32, i32, i32, i32, i32, i32, i32, i32, vp]),
     "launch_copy_blocks": (None, [vp, vp, vp, i32, i32, i32, i32, vp]),
     "swiftllm_hip_launch_copy_blocks": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, vp]),
     "swiftllm_hip_copy_blocks": (i32, [vp, vp, vp, sz, sz, sz, sz, sz, vp]),

@@ -23,7 +23,7 @@ LIB = PKG / "libswiftllm_hip.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["abi.cpp", "paged_attention.hip", "cache_ops.hip", "block_copy.hip", "moe.hip", "moe_experts.hip"]
+SOURCES = ["abi.cpp", "paged_attention.hip", "prefill.hip", "cache_ops.hip", "block_copy.hip", "moe.hip", "moe_experts.hip"]
 
 FLAGS = [
     "-O3",

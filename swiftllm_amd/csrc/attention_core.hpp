@@ -1,0 +1,177 @@
+// Device building blocks shared by the paged-attention kernels (decode and
+// prefill): KV tile loads in the [NB, Hkv, D, 16] layout and the per-block
+// MFMA attention step with an online softmax.
+#pragma once
+
+#include "common.hpp"
+
+namespace swiftllm {
+namespace attn {
+
+constexpr float kLog2e = 1.4426950408889634f;
+// Probabilities are produced as 2^kPExp * exp2(s - m) (<= 2^15 < 65504).
+constexpr float kPExp = 15.0f;
+
+__device__ __forceinline__ f4 mfma16(h4 a, h4 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ h4 mask_h4(h4 v, unsigned long long m) {
+    return __builtin_bit_cast(h4, __builtin_bit_cast(unsigned long long, v) & m);
+}
+
+__device__ __forceinline__ h4 to_h4(f4 v) {
+    h4 r;
+    r[0] = static_cast<f16>(v[0]);
+    r[1] = static_cast<f16>(v[1]);
+    r[2] = static_cast<f16>(v[2]);
+    r[3] = static_cast<f16>(v[3]);
+    return r;
+}
+
+// A block id names a block of the pool: never negative, and below the pool
+// size when that is known (num_blocks > 0).
+__device__ __forceinline__ bool block_ok(int b, int num_blocks) {
+    return b >= 0 && (num_blocks <= 0 || b < num_blocks);
+}
+
+// Decode reads each KV tile once per call, so it loads them nontemporally
+// (streamed past the caches instead of evicting Q, block tables and the
+// other waves' prefetched tiles; config 2: 113.0 us -> 104.9 us per call).
+// Prefill reads each tile once per query group and keeps them cached (NT =
+// false).
+template <bool NT>
+__device__ __forceinline__ h4 load_kv(const f16* p) {
+    if (NT) return __builtin_nontemporal_load(reinterpret_cast<const h4*>(p));
+    return *reinterpret_cast<const h4*>(p);
+}
+
+template <int D, bool NT = true>
+__device__ __forceinline__ void load_tile(const f16* kc, const f16* vc, int Hkv, int num_blocks,
+                                          int b, int kvh, int loff, h4 (&k)[D / 16],
+                                          h4 (&v)[D / 16]) {
+    constexpr int NJ = D / 16;
+    // An id outside the pool reads block 0 instead (in bounds); the caller
+    // skips such a block.
+    const int bsafe = block_ok(b, num_blocks) ? b : 0;
+    const size_t base = kv_tile_offset(bsafe, kvh, Hkv, D) + loff;
+    const f16* kp = kc + base;
+    const f16* vp = vc + base;
+#pragma unroll
+    for (int J = 0; J < NJ; ++J) {
+        k[J] = load_kv<NT>(kp + kv_elem_offset(16 * J, 0));
+    }
+#pragma unroll
+    for (int J = 0; J < NJ; ++J) {
+        v[J] = load_kv<NT>(vp + kv_elem_offset(16 * J, 0));
+    }
+}
+
+// Q^T operand of step 2: lane (r, kg) holds q[h0 + r][16J + 4kg .. +3].
+template <int D>
+struct QOperand {
+    h4 v[D / 16];
+    __device__ __forceinline__ h4 get(int J) const { return v[J]; }
+};
+
+// Running softmax state of one wave: max (log2 domain), sum of
+// 2^15 * exp2(s - max) over this lane's token rows, and O^T accumulators.
+template <int D>
+struct WaveState {
+    float m;
+    float l;
+    f4 acc[D / 16];
+};
+
+// One 16-token block for the wave's 16 query rows (MFMA N side), all on
+// v_mfma_f32_16x16x16_f16:
+//   1. the K tile rows arrive tokens-contiguous ([d][t]); an MFMA against a
+//      0/1 identity operand returns them in the transposed ([t][d]) register
+//      layout, exactly (one product per output);
+//   2. S^T[t][g] = sum_d K^T[t][d] Q^T[d][g];
+//   3. online softmax in fp32 in the log2 domain; the 4 token rows of query
+//      row g live in lanes g, g^16, g^32, g^48 (two xor shuffles);
+//   4. O^T[d][g] += V[d][t] P^T[t][g] with V in its stored layout and P fed
+//      as fp16 hi + lo parts (~22 bits), P = 2^15 * exp2(s - m).
+// The first nv tokens of the tile exist (the rest is zeroed so stale values
+// cannot reach a sum; nv == 0: the block contributes nothing), and query row
+// g = lane % 16 of this lane sees tokens t < lim (lim <= nv).
+template <int D>
+__device__ __forceinline__ void attend_block(WaveState<D>& st, int nv, int lim, int kg,
+                                             h4 (&kA)[D / 16], h4 (&vA)[D / 16],
+                                             const QOperand<D>& qB, h4 ident,
+                                             float scale_log2) {
+    constexpr int NJ = D / 16;
+    if (nv < kBlockTokens) {
+        // Tail block: zero the K/V of tokens past the context so no stale
+        // value (possibly NaN) reaches a sum through a 0 weight.
+        const int c = min(max(nv - 4 * kg, 0), 4);
+        const unsigned long long m = (c >= 4) ? ~0ull : ((1ull << (16 * c)) - 1ull);
+#pragma unroll
+        for (int J = 0; J < NJ; ++J) {
+            kA[J] = mask_h4(kA[J], m);
+            vA[J] = mask_h4(vA[J], m);
+        }
+    }
+    // Steps 1 + 2.
+    f4 s0 = f4{0, 0, 0, 0}, s1 = f4{0, 0, 0, 0};
+#pragma unroll
+    for (int J = 0; J < NJ; ++J) {
+        const f4 t = mfma16(kA[J], ident, f4{0, 0, 0, 0});
+        const h4 kT = to_h4(t);
+        if (J & 1) {
+            s1 = mfma16(kT, qB.get(J), s1);
+        } else {
+            s0 = mfma16(kT, qB.get(J), s0);
+        }
+    }
+    // Step 3. Lane (r, kg) holds S^T[t = 4kg + i][g = r].
+    float sv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        sv[i] = (s0[i] + s1[i]) * scale_log2;
+        if (4 * kg + i >= lim) sv[i] = -INFINITY;
+    }
+    float bm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    bm = fmaxf(bm, __shfl_xor(bm, 16));
+    bm = fmaxf(bm, __shfl_xor(bm, 32));
+    if (__any(bm > st.m)) {
+        const float m_new = fmaxf(st.m, bm);
+        const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
+#pragma unroll
+        for (int J = 0; J < NJ; ++J) st.acc[J] *= alpha;
+        st.l *= alpha;
+        st.m = m_new;
+    }
+    // While no valid token has been seen (an out-of-pool block, nv == 0) the
+    // max is still -inf and every sv is -inf: use 0 so the weights are 0.
+    const float m_use = (st.m == -INFINITY) ? 0.0f : st.m;
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(sv[i] - m_use + kPExp);
+    st.l += (p[0] + p[1]) + (p[2] + p[3]);
+    h4 ph, pl;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        ph[i] = static_cast<f16>(p[i]);
+        pl[i] = static_cast<f16>(p[i] - static_cast<float>(ph[i]));
+    }
+    // Step 4. Lane (r, kg) accumulates O^T[d = 16J + 4kg + i][g = r].
+#pragma unroll
+    for (int J = 0; J < NJ; ++J) {
+        st.acc[J] = mfma16(vA[J], ph, st.acc[J]);
+        st.acc[J] = mfma16(vA[J], pl, st.acc[J]);
+    }
+}
+
+// Every query row sees the same nv tokens (decode).
+template <int D>
+__device__ __forceinline__ void attend_block(WaveState<D>& st, int nv, int kg,
+                                             h4 (&kA)[D / 16], h4 (&vA)[D / 16],
+                                             const QOperand<D>& qB, h4 ident,
+                                             float scale_log2) {
+    attend_block<D>(st, nv, nv, kg, kA, vA, qB, ident, scale_log2);
+}
+
+}  // namespace attn
+}  // namespace swiftllm

@@ -38,14 +38,12 @@
 #include <algorithm>
 #include <cmath>
 
-#include "common.hpp"
+#include "attention_core.hpp"
 
 namespace swiftllm {
 namespace {
 
-constexpr float kLog2e = 1.4426950408889634f;
-// Probabilities are produced as 2^kPExp * exp2(s - m) (<= 2^15 < 65504).
-constexpr float kPExp = 15.0f;
+using namespace attn;
 
 struct DecodeArgs {
     f16* out;
@@ -68,149 +66,6 @@ struct DecodeArgs {
     int MP;           // partitions per sequence in the workspace
     int snake;        // > 0: single-pass item order in snake rounds of this many
 };
-
-__device__ __forceinline__ f4 mfma16(h4 a, h4 b, f4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ h4 mask_h4(h4 v, unsigned long long m) {
-    return __builtin_bit_cast(h4, __builtin_bit_cast(unsigned long long, v) & m);
-}
-
-__device__ __forceinline__ h4 to_h4(f4 v) {
-    h4 r;
-    r[0] = static_cast<f16>(v[0]);
-    r[1] = static_cast<f16>(v[1]);
-    r[2] = static_cast<f16>(v[2]);
-    r[3] = static_cast<f16>(v[3]);
-    return r;
-}
-
-__device__ __forceinline__ bool block_ok(int b, int num_blocks) {
-    return num_blocks <= 0 || static_cast<unsigned>(b) < static_cast<unsigned>(num_blocks);
-}
-
-// KV tiles are read once per call, so they are loaded nontemporally (streamed
-// past the caches instead of evicting Q, block tables and the other waves'
-// prefetched tiles). Measured on config 2: 113.0 us -> 104.9 us per call.
-#ifndef SWIFTLLM_KV_NONTEMPORAL
-#define SWIFTLLM_KV_NONTEMPORAL 1
-#endif
-
-__device__ __forceinline__ h4 load_kv(const f16* p) {
-#if SWIFTLLM_KV_NONTEMPORAL
-    return __builtin_nontemporal_load(reinterpret_cast<const h4*>(p));
-#else
-    return *reinterpret_cast<const h4*>(p);
-#endif
-}
-
-template <int D>
-__device__ __forceinline__ void load_tile(const f16* kc, const f16* vc, int Hkv, int num_blocks,
-                                          int b, int kvh, int loff, h4 (&k)[D / 16],
-                                          h4 (&v)[D / 16]) {
-    constexpr int NJ = D / 16;
-    // An id outside the pool reads block 0 instead (in bounds); the caller
-    // skips such a block.
-    const int bsafe = block_ok(b, num_blocks) ? b : 0;
-    const size_t base = kv_tile_offset(bsafe, kvh, Hkv, D) + loff;
-    const f16* kp = kc + base;
-    const f16* vp = vc + base;
-#pragma unroll
-    for (int J = 0; J < NJ; ++J) {
-        k[J] = load_kv(kp + kv_elem_offset(16 * J, 0));
-    }
-#pragma unroll
-    for (int J = 0; J < NJ; ++J) {
-        v[J] = load_kv(vp + kv_elem_offset(16 * J, 0));
-    }
-}
-
-// Q^T operand of step 2: lane (r, kg) holds q[h0 + r][16J + 4kg .. +3].
-template <int D>
-struct QOperand {
-    h4 v[D / 16];
-    __device__ __forceinline__ h4 get(int J) const { return v[J]; }
-};
-
-// Running softmax state of one wave: max (log2 domain), sum of
-// 2^15 * exp2(s - max) over this lane's token rows, and O^T accumulators.
-template <int D>
-struct WaveState {
-    float m;
-    float l;
-    f4 acc[D / 16];
-};
-
-// Steps 1-4 of the header for one block whose first nv tokens are valid
-// (nv == 0: the block contributes nothing).
-template <int D>
-__device__ __forceinline__ void attend_block(WaveState<D>& st, int nv, int kg,
-                                             h4 (&kA)[D / 16], h4 (&vA)[D / 16],
-                                             const QOperand<D>& qB, h4 ident,
-                                             float scale_log2) {
-    constexpr int NJ = D / 16;
-    if (nv < kBlockTokens) {
-        // Tail block: zero the K/V of tokens past the context so no stale
-        // value (possibly NaN) reaches a sum through a 0 weight.
-        const int c = min(max(nv - 4 * kg, 0), 4);
-        const unsigned long long m = (c >= 4) ? ~0ull : ((1ull << (16 * c)) - 1ull);
-#pragma unroll
-        for (int J = 0; J < NJ; ++J) {
-            kA[J] = mask_h4(kA[J], m);
-            vA[J] = mask_h4(vA[J], m);
-        }
-    }
-    // Steps 1 + 2.
-    f4 s0 = f4{0, 0, 0, 0}, s1 = f4{0, 0, 0, 0};
-#pragma unroll
-    for (int J = 0; J < NJ; ++J) {
-        const f4 t = mfma16(kA[J], ident, f4{0, 0, 0, 0});
-        const h4 kT = to_h4(t);
-        if (J & 1) {
-            s1 = mfma16(kT, qB.get(J), s1);
-        } else {
-            s0 = mfma16(kT, qB.get(J), s0);
-        }
-    }
-    // Step 3. Lane (r, kg) holds S^T[t = 4kg + i][g = r].
-    float sv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        sv[i] = (s0[i] + s1[i]) * scale_log2;
-        if (4 * kg + i >= nv) sv[i] = -INFINITY;
-    }
-    float bm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-    bm = fmaxf(bm, __shfl_xor(bm, 16));
-    bm = fmaxf(bm, __shfl_xor(bm, 32));
-    if (__any(bm > st.m)) {
-        const float m_new = fmaxf(st.m, bm);
-        const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
-#pragma unroll
-        for (int J = 0; J < NJ; ++J) st.acc[J] *= alpha;
-        st.l *= alpha;
-        st.m = m_new;
-    }
-    // While no valid token has been seen (an out-of-pool block, nv == 0) the
-    // max is still -inf and every sv is -inf: use 0 so the weights are 0.
-    const float m_use = (st.m == -INFINITY) ? 0.0f : st.m;
-    float p[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(sv[i] - m_use + kPExp);
-    st.l += (p[0] + p[1]) + (p[2] + p[3]);
-    h4 ph, pl;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        ph[i] = static_cast<f16>(p[i]);
-        pl[i] = static_cast<f16>(p[i] - static_cast<float>(ph[i]));
-    }
-    // Step 4. Lane (r, kg) accumulates O^T[d = 16J + 4kg + i][g = r].
-#pragma unroll
-    for (int J = 0; J < NJ; ++J) {
-        st.acc[J] = mfma16(vA[J], ph, st.acc[J]);
-        st.acc[J] = mfma16(vA[J], pl, st.acc[J]);
-    }
-}
 
 // Attends `count` blocks of one sequence: logical blocks first,
 // first + stride, ... Blocks are double-buffered in registers, so the next

@@ -1,0 +1,266 @@
+// Paged prefill attention for gfx950.
+//
+// Contract (crates/swiftllm-cuda/src/bindings.rs:33-54 declares the launch;
+// crates/swiftllm-core/src/memory/paged_attention.rs:154-189 lists the steps:
+// scores Q K^T / sqrt(d), causal mask, softmax, times V, with K and V stored
+// into the cache by slot_mapping). The reference computes none of it. Here:
+//   the query tokens of the batch are packed: sequence s owns tokens
+//   [start_s, start_s + L_s), start_s = sum of context_lens before s, and
+//   token p of s sits in the cache at slot_mapping[start_s + p] (the caller
+//   writes K/V there first, e.g. with reshape_and_cache);
+//   out[start_s + i, h] = sum_{j <= i} softmax_j(scale q[start_s + i, h] .
+//                         K(slot[start_s + j], kvh)) V(slot[start_s + j], kvh)
+//   with kvh = h / (H / Hkv). fp16 in and out, fp32 accumulation.
+// The slots of a sequence must follow its block table from position 0
+// (slot of p = table[p / 16] * 16 + p % 16, what get_slot_mapping produces):
+// the kernel reads the block of 16 positions from the slot of the first.
+//
+// Work decomposition. A wave owns 16 MFMA query rows: tpw = 16 / gw
+// consecutive query tokens times gw = min(G, 16) query heads of one kv head,
+// so every K/V tile it loads serves all of them. It walks the key blocks up
+// to its last token with the decode kernel's per-block MFMA step; each lane's
+// query row carries its own causal limit. A wave's rows are complete when its
+// walk ends, so it writes its outputs directly: no combine, no barriers.
+// Four waves per workgroup take consecutive token groups; workgroups go out
+// latest tokens first (the longest walks start first). K/V tiles are loaded
+// with ordinary (cached) loads: every query group of a sequence re-reads them.
+
+#include "attention_core.hpp"
+
+namespace swiftllm {
+namespace {
+
+using namespace attn;
+
+constexpr int kPrefillWaves = 4;
+
+struct PrefillArgs {
+    f16* out;            // [T][H][D]
+    const f16* q;        // [T][H][D]
+    const f16* kc;
+    const f16* vc;
+    const int* slots;    // [T]
+    const int* ctx;      // [S] query tokens per sequence
+    float scale_log2;
+    int S;
+    int H;
+    int Hkv;
+    int G;               // query heads per kv head
+    int nhc;             // head chunks of 16 per kv head
+    int gw;              // query heads per row group: min(G, 16)
+    int tpw;             // query tokens per wave: 16 / gw
+    int groups;          // workgroups per (sequence, kv head chunk) in the grid
+    int num_blocks;      // bound on block ids; <= 0: unbounded
+};
+
+template <int D>
+__global__ __launch_bounds__(64 * kPrefillWaves) __attribute__((amdgpu_waves_per_eu(2)))
+void paged_prefill_kernel(const PrefillArgs a) {
+    constexpr int NJ = D / 16;
+    __shared__ int s_part[kPrefillWaves];
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15;
+    const int kg = lane >> 4;
+    const int s = blockIdx.z;
+    const int kvh = blockIdx.y / a.nhc;
+    const int hc = blockIdx.y - kvh * a.nhc;
+    const int gi = a.groups - 1 - static_cast<int>(blockIdx.x);  // latest tokens first
+
+    // start_s = sum of the lengths before s (all threads share the sum).
+    int part = 0;
+    for (int i = threadIdx.x; i < s; i += 64 * kPrefillWaves) part += max(a.ctx[i], 0);
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) part += __shfl_xor(part, d);
+    if (lane == 0) s_part[w] = part;
+    __syncthreads();
+    int start = 0;
+#pragma unroll
+    for (int i = 0; i < kPrefillWaves; ++i) start += s_part[i];
+    const int L = max(a.ctx[s], 0);
+
+    const int tq0 = (gi * kPrefillWaves + w) * a.tpw;  // first query token of this wave
+    if (tq0 >= L) return;
+    const int tq_last = min(tq0 + a.tpw, L) - 1;
+
+    // Query row r: token tq0 + r / gw, head h0 + r % gw.
+    const int rt = r / a.gw;
+    const int rh = r - rt * a.gw;
+    const int g = hc * 16 + rh;
+    const int tq = tq0 + rt;
+    const bool row_ok = (rt < a.tpw) && (tq < L) && (g < a.G);
+    const int h = kvh * a.G + min(g, a.G - 1);
+    const size_t qrow = (static_cast<size_t>(start) + min(tq, L - 1)) * a.H + h;
+
+    QOperand<D> qB;
+    {
+        const f16* qp = a.q + qrow * D + 4 * kg;
+#pragma unroll
+        for (int J = 0; J < NJ; ++J) {
+            const h4 v = *reinterpret_cast<const h4*>(qp + 16 * J);
+            qB.v[J] = row_ok ? v : h4{0, 0, 0, 0};
+        }
+    }
+    h4 ident;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        ident[i] = (4 * kg + i == r) ? static_cast<f16>(1.0f) : static_cast<f16>(0.0f);
+    }
+    const int loff = kv_elem_offset(r, 4 * kg);
+    const const_int* srow = as_const(a.slots) + start;
+
+    WaveState<D> st;
+    st.m = -INFINITY;
+    st.l = 0.0f;
+#pragma unroll
+    for (int J = 0; J < NJ; ++J) st.acc[J] = f4{0, 0, 0, 0};
+
+    // Key blocks 0 .. nkb-1, double-buffered like the decode walk: the
+    // steady loop runs while at least three blocks are left (both loads of
+    // an iteration are real blocks, no load depends on a condition), and the
+    // last one or two are peeled off.
+    const int nkb = tq_last / kBlockTokens + 1;
+    auto block_at = [&](int jb) {
+        return __builtin_amdgcn_readfirstlane(srow[jb * kBlockTokens]) / kBlockTokens;
+    };
+    auto attend = [&](int jb, int b, h4 (&k)[NJ], h4 (&v)[NJ]) {
+        const int base = jb * kBlockTokens;
+        const int nv = block_ok(b, a.num_blocks) ? min(kBlockTokens, L - base) : 0;
+        const int lim = row_ok ? min(max(tq + 1 - base, 0), nv) : 0;
+        attend_block<D>(st, nv, lim, kg, k, v, qB, ident, a.scale_log2);
+    };
+    {
+        h4 kA[NJ], vA[NJ], kB[NJ], vB[NJ];
+        int jA = 0;
+        int bA = block_at(0);
+        load_tile<D, false>(a.kc, a.vc, a.Hkv, a.num_blocks, bA, kvh, loff, kA, vA);
+        int left = nkb;
+        for (; left > 2; left -= 2) {
+            const int jB = jA + 1;
+            const int bB = block_at(jB);
+            load_tile<D, false>(a.kc, a.vc, a.Hkv, a.num_blocks, bB, kvh, loff, kB, vB);
+            attend(jA, bA, kA, vA);
+            jA = jB + 1;
+            bA = block_at(jA);
+            load_tile<D, false>(a.kc, a.vc, a.Hkv, a.num_blocks, bA, kvh, loff, kA, vA);
+            attend(jB, bB, kB, vB);
+        }
+        if (left == 2) {
+            const int jB = jA + 1;
+            const int bB = block_at(jB);
+            load_tile<D, false>(a.kc, a.vc, a.Hkv, a.num_blocks, bB, kvh, loff, kB, vB);
+            attend(jA, bA, kA, vA);
+            attend(jB, bB, kB, vB);
+        } else {
+            attend(jA, bA, kA, vA);
+        }
+    }
+
+    float l_run = st.l;
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
+    if (!row_ok) return;
+    const float inv = (l_run > 0.0f) ? 1.0f / l_run : 0.0f;
+    f16* op = a.out + qrow * D + 4 * kg;
+#pragma unroll
+    for (int J = 0; J < NJ; ++J) {
+        h4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = static_cast<f16>(st.acc[J][i] * inv);
+        *reinterpret_cast<h4*>(op + 16 * J) = o;
+    }
+}
+
+int prefill(const char* who, void* out, const void* q, const void* kc, const void* vc,
+            const int* slots, const int* ctx, float scale, long long S, long long H, long long Hkv,
+            long long D, long long BS, long long max_len, int num_blocks, hipStream_t stream) {
+    if (S < 0 || H <= 0 || Hkv <= 0 || D <= 0 || BS <= 0 || max_len < 0) {
+        return fail(SWIFTLLM_ERR_INVALID_PARAMETER,
+                    "%s: num_seqs=%lld num_heads=%lld num_kv_heads=%lld head_dim=%lld "
+                    "block_size=%lld max_context_len=%lld", who, S, H, Hkv, D, BS, max_len);
+    }
+    if (H % Hkv != 0) {
+        return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: num_heads %lld not a multiple of num_kv_heads %lld",
+                    who, H, Hkv);
+    }
+    if ((D != 64 && D != 128) || BS != kBlockTokens) {
+        return fail(SWIFTLLM_ERR_NOT_SUPPORTED, "%s: head_dim=%lld block_size=%lld (supported: 64/128, 16)",
+                    who, D, BS);
+    }
+    if (S > 65535 || H > 65535 || max_len > (1LL << 30)) {
+        return fail(SWIFTLLM_ERR_NOT_SUPPORTED, "%s: num_seqs=%lld num_heads=%lld max_context_len=%lld",
+                    who, S, H, max_len);
+    }
+    if (S > 0 && max_len > 0 && (!out || !q || !kc || !vc || !slots || !ctx)) {
+        return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: null pointer", who);
+    }
+    if (!aligned(out, 8) || !aligned(q, 8) || !aligned(kc, 8) || !aligned(vc, 8) ||
+        !aligned(slots, 4) || !aligned(ctx, 4)) {
+        return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: misaligned pointer", who);
+    }
+    int rc = require_device();
+    if (rc != SWIFTLLM_OK) return rc;
+    if (S == 0 || max_len == 0) return ok();
+    PrefillArgs a{};
+    a.out = static_cast<f16*>(out);
+    a.q = static_cast<const f16*>(q);
+    a.kc = static_cast<const f16*>(kc);
+    a.vc = static_cast<const f16*>(vc);
+    a.slots = slots;
+    a.ctx = ctx;
+    a.scale_log2 = static_cast<float>(static_cast<double>(scale) * static_cast<double>(kLog2e));
+    a.S = static_cast<int>(S);
+    a.H = static_cast<int>(H);
+    a.Hkv = static_cast<int>(Hkv);
+    a.G = a.H / a.Hkv;
+    a.nhc = (a.G + 15) / 16;
+    a.gw = a.G < 16 ? a.G : 16;
+    a.tpw = 16 / a.gw;
+    const long long per_wg = static_cast<long long>(kPrefillWaves) * a.tpw;
+    a.groups = static_cast<int>((max_len + per_wg - 1) / per_wg);
+    a.num_blocks = num_blocks;
+    const dim3 grid(static_cast<unsigned>(a.groups), static_cast<unsigned>(a.Hkv * a.nhc),
+                    static_cast<unsigned>(S));
+    const hipError_t err = D == 128
+        ? launch(paged_prefill_kernel<128>, grid, dim3(64 * kPrefillWaves), 0, stream, a)
+        : launch(paged_prefill_kernel<64>, grid, dim3(64 * kPrefillWaves), 0, stream, a);
+    return launched(err, who);
+}
+
+}  // namespace
+}  // namespace swiftllm
+
+using namespace swiftllm;
+
+extern "C" {
+
+int swiftllm_hip_paged_attention_prefill(void* output, const void* query, const void* key_cache,
+                                         const void* value_cache, const int32_t* slot_mapping,
+                                         const int32_t* context_lens,
+                                         const swiftllm_paged_attention_params* p,
+                                         hipStream_t stream) {
+    const char* who = "swiftllm_hip_paged_attention_prefill";
+    if (p == nullptr) return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: null params", who);
+    const size_t lim = 0x7fffffff;
+    if (p->num_seqs > lim || p->num_heads > lim || p->num_kv_heads > lim || p->head_dim > lim ||
+        p->block_size > lim || p->max_context_len > lim) {
+        return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: parameter out of range", who);
+    }
+    return prefill(who, output, query, key_cache, value_cache, slot_mapping, context_lens, p->scale,
+                   static_cast<long long>(p->num_seqs), static_cast<long long>(p->num_heads),
+                   static_cast<long long>(p->num_kv_heads), static_cast<long long>(p->head_dim),
+                   static_cast<long long>(p->block_size), static_cast<long long>(p->max_context_len),
+                   0, stream);
+}
+
+int swiftllm_hip_launch_paged_prefill(void* output, const void* query, const void* key_cache,
+                                      const void* value_cache, const int32_t* slot_mapping,
+                                      const int32_t* context_lens, float scale, int num_seqs,
+                                      int num_heads, int num_kv_heads, int head_dim, int block_size,
+                                      int max_context_len, int num_blocks, hipStream_t stream) {
+    return prefill("swiftllm_hip_launch_paged_prefill", output, query, key_cache, value_cache,
+                   slot_mapping, context_lens, scale, num_seqs, num_heads, num_kv_heads, head_dim,
+                   block_size, max_context_len, num_blocks, stream);
+}
+
+}  // extern "C"

@@ -137,6 +137,17 @@ def paged_attention_decode(output: Ptr, query: Ptr, key_cache: Ptr, value_cache:
         _p(context_lens), ctypes.byref(c), _s(stream)))
 
 
+def paged_attention_prefill(output: Ptr, query: Ptr, key_cache: Ptr, value_cache: Ptr,
+                            slot_mapping: Ptr, context_lens: Ptr, params: PagedAttentionParams,
+                            stream: Optional[Stream] = None) -> None:
+    """bindings.rs:32-54: causal attention over packed prompts whose K/V are
+    already in the cache at slot_mapping."""
+    c = params.to_c()
+    check_status(_lib.lib().swiftllm_hip_paged_attention_prefill(
+        _p(output), _p(query), _p(key_cache), _p(value_cache), _p(slot_mapping),
+        _p(context_lens), ctypes.byref(c), _s(stream)))
+
+
 def reshape_and_cache(key: Ptr, value: Ptr, key_cache: Ptr, value_cache: Ptr, slot_mapping: Ptr,
                       params: ReshapeCacheParams, stream: Optional[Stream] = None) -> None:
     """bindings.rs:94-113."""
@@ -228,6 +239,17 @@ def paged_attention_v2(output: Ptr, ws: DeviceArray, query: Ptr, key_cache: Ptr,
         _p(output), ws.ptr, ws.nbytes, _p(query), _p(key_cache), _p(value_cache),
         _p(block_tables), _p(context_lens), scale, num_seqs, num_heads, num_kv_heads, head_dim,
         block_size, max_num_blocks_per_seq, partition_size, num_blocks, _s(stream)))
+
+
+def launch_paged_prefill(output: Ptr, query: Ptr, key_cache: Ptr, value_cache: Ptr,
+                         slot_mapping: Ptr, context_lens: Ptr, scale: float, num_seqs: int,
+                         num_heads: int, num_kv_heads: int, head_dim: int, block_size: int,
+                         max_context_len: int, num_blocks: int = 0,
+                         stream: Optional[Stream] = None) -> None:
+    check_status(_lib.lib().swiftllm_hip_launch_paged_prefill(
+        _p(output), _p(query), _p(key_cache), _p(value_cache), _p(slot_mapping),
+        _p(context_lens), scale, num_seqs, num_heads, num_kv_heads, head_dim, block_size,
+        max_context_len, num_blocks, _s(stream)))
 
 
 def launch_reshape_and_cache(key: Ptr, value: Ptr, key_cache: Ptr, value_cache: Ptr,
@@ -330,6 +352,34 @@ class PagedAttention:
                                  num_blocks=key_cache.shape[0], stream=stream)
         if stream is not None:
             stream.synchronize()
+
+    def prefill(self, query: DeviceArray, key: DeviceArray, value: DeviceArray,
+                key_cache: DeviceArray, value_cache: DeviceArray, slot_mapping: Sequence[int],
+                stream: Optional[Stream] = None) -> DeviceArray:
+        """paged_attention.rs:154-189. query [B,S,H,D], key/value [B,S,Hkv,D]
+        fp16 on the device, slot_mapping of the B*S tokens; stores K/V (step 5)
+        and returns the causal attention output [B,S,H,D] (steps 1-4)."""
+        self._validate()
+        if len(query.shape) != 4 or len(key.shape) != 4:
+            raise InvalidParameter(f"query and key must be 4-d, got {len(query.shape)}-d "
+                                   f"and {len(key.shape)}-d")
+        B, S, H, D = query.shape
+        c = self.config
+        if H != c.num_heads or D != c.head_dim:
+            raise InvalidParameter(f"query [.., {H}, {D}] vs config heads {c.num_heads} dim {c.head_dim}")
+        self.reshape_and_cache(key, value, key_cache, value_cache, slot_mapping, stream)
+        out = DeviceArray((B, S, H, D), np.float16)
+        sm = DeviceArray.from_numpy(np.asarray(slot_mapping, dtype=np.int32))
+        ctx = DeviceArray.from_numpy(np.full(B, S, dtype=np.int32))
+        launch_paged_prefill(out, query, key_cache, value_cache, sm, ctx, c.scale, B, H,
+                             c.num_kv_heads, D, c.block_size, S, num_blocks=key_cache.shape[0],
+                             stream=stream)
+        if stream is not None:
+            stream.synchronize()
+        else:
+            from ._hip import synchronize
+            synchronize()
+        return out
 
     def decode(self, query: DeviceArray, key: DeviceArray, value: DeviceArray,
                key_cache: DeviceArray, value_cache: DeviceArray,

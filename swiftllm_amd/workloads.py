@@ -137,6 +137,66 @@ def decode_config(cfg: int, seed: int = 0, *, num_seqs: Optional[int] = None,
 
 
 @dataclass
+class PrefillWorkload:
+    q: np.ndarray             # fp16 [T, H, D] packed prompts
+    key_cache: np.ndarray     # fp16 [NB, Hkv, D, BS], the prompts' K/V already written
+    value_cache: np.ndarray
+    slot_mapping: np.ndarray  # int32 [T]
+    context_lens: np.ndarray  # int32 [S] prompt lengths
+    key: np.ndarray           # fp16 [T, Hkv, D] (what was written)
+    value: np.ndarray
+    scale: float
+
+    @property
+    def num_tokens(self) -> int:
+        return self.q.shape[0]
+
+    def flops(self) -> int:
+        """QK^T and PV multiply-adds of the causal attention."""
+        T, H, D = self.q.shape
+        pairs = sum(int(L) * (int(L) + 1) // 2 for L in self.context_lens)
+        return 4 * pairs * H * D
+
+    def bytes(self) -> int:
+        """Q in, O out, K/V read once per sequence and kv head."""
+        T, H, D = self.q.shape
+        Hkv = self.key_cache.shape[1]
+        return 2 * T * H * D * 2 + 2 * T * Hkv * D * 2 + self.slot_mapping.nbytes
+
+
+def prefill_config(lens, num_heads: int = 32, num_kv_heads: int = 8, head_dim: int = 128,
+                   seed: int = 0, std: float = 0.5, poison: bool = True) -> PrefillWorkload:
+    """Packed prompts of the given lengths over a randomly permuted block pool
+    (1.25x the blocks needed); slots walk each prompt's table from position 0
+    (kv_cache.rs:186-216). Unused cache slots hold NaN when `poison`."""
+    rng = np.random.default_rng(seed)
+    lens = np.asarray(lens, dtype=np.int32)
+    T = int(lens.sum())
+    need = int(((lens + BLOCK_SIZE - 1) // BLOCK_SIZE).sum())
+    NB = max(int(math.ceil(1.25 * need)), 1)
+    perm = rng.permutation(NB)
+    slots, k = [], 0
+    for L in lens:
+        nb = (int(L) + BLOCK_SIZE - 1) // BLOCK_SIZE
+        table = perm[k:k + nb]
+        k += nb
+        slots.extend(int(table[p // BLOCK_SIZE]) * BLOCK_SIZE + p % BLOCK_SIZE for p in range(int(L)))
+    slots = np.asarray(slots, dtype=np.int32)
+    Hkv, D = num_kv_heads, head_dim
+    fill = np.nan if poison else 0.0
+    kc = np.full((NB, Hkv, D, BLOCK_SIZE), fill, np.float16)
+    vc = np.full((NB, Hkv, D, BLOCK_SIZE), fill, np.float16)
+    key = _normal_f16(rng, (T, Hkv, D), std)
+    value = _normal_f16(rng, (T, Hkv, D), std)
+    b, o = slots // BLOCK_SIZE, slots % BLOCK_SIZE
+    kc[b, :, :, o] = key
+    vc[b, :, :, o] = value
+    q = _normal_f16(rng, (T, num_heads, D), std)
+    return PrefillWorkload(q=q, key_cache=kc, value_cache=vc, slot_mapping=slots,
+                           context_lens=lens, key=key, value=value, scale=1.0 / math.sqrt(D))
+
+
+@dataclass
 class MoeWorkload:
     x: np.ndarray        # fp16 [T, hidden]
     logits: np.ndarray   # fp32 [T, E]

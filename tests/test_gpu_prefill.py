@@ -1,0 +1,104 @@
+"""Paged prefill on the GPU against oracle.prefill_numpy (float64), to the
+attention tolerance (max_abs <= 2e-3, max_rel <= 1e-2 with a 1e-3 floor):
+packed prompts of ragged lengths around block edges, GQA groups from 1 to
+32, head_dim 64 and 128, NaN in every unused cache slot, the bounded status
+entry, the bindings twin and PagedAttention.prefill."""
+
+import numpy as np
+import pytest
+
+import oracle
+from helpers import assert_attention_close
+from swiftllm_amd import paged_attention as pa
+from swiftllm_amd import workloads
+from swiftllm_amd._hip import DeviceArray, synchronize
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(w, entry="status", max_len=None):
+    T, H, D = w.q.shape
+    Hkv = w.key_cache.shape[1]
+    S = len(w.context_lens)
+    max_len = int(w.context_lens.max()) if max_len is None else max_len
+    out = DeviceArray((T, H, D), np.float16)
+    out.fill_byte(0xFF)
+    q = DeviceArray.from_numpy(w.q)
+    kc, vc = DeviceArray.from_numpy(w.key_cache), DeviceArray.from_numpy(w.value_cache)
+    sm, ctx = DeviceArray.from_numpy(w.slot_mapping), DeviceArray.from_numpy(w.context_lens)
+    if entry == "status":
+        pa.launch_paged_prefill(out, q, kc, vc, sm, ctx, w.scale, S, H, Hkv, D, 16, max_len,
+                                num_blocks=w.key_cache.shape[0])
+    else:
+        pa.paged_attention_prefill(out, q, kc, vc, sm, ctx,
+                                   pa.PagedAttentionParams(S, H, Hkv, D, 16, w.scale, max_len))
+    synchronize()
+    return out.numpy()
+
+
+def _ref(w):
+    return oracle.prefill_numpy(w.q, w.key_cache, w.value_cache, w.slot_mapping, w.context_lens,
+                                w.scale)
+
+
+@pytest.mark.parametrize("H,Hkv,D", [(32, 8, 128), (8, 8, 64), (64, 8, 128), (16, 1, 64),
+                                     (32, 1, 128), (12, 4, 64)])
+def test_prefill_gqa_shapes(dev, H, Hkv, D):
+    lens = (1, 15, 16, 17, 70, 129)
+    w = workloads.prefill_config(lens, H, Hkv, D, seed=H * 10 + Hkv + D)
+    assert_attention_close(_run(w), _ref(w), f"prefill H{H} Hkv{Hkv} D{D}")
+
+
+@pytest.mark.parametrize("entry", ["status", "params"])
+def test_prefill_long_prompts(dev, entry):
+    """Llama-3-8B layer heads, two long prompts and a short one."""
+    w = workloads.prefill_config((1024, 517, 3), 32, 8, 128, seed=7)
+    assert_attention_close(_run(w, entry), _ref(w), f"prefill long {entry}")
+
+
+def test_prefill_empty_and_zero_length_sequences(dev):
+    w = workloads.prefill_config((0, 33, 0, 5), 8, 2, 64, seed=8)
+    out = _run(w)
+    assert_attention_close(out, _ref(w), "prefill with empty prompts")
+
+
+def test_prefill_max_len_above_every_prompt(dev):
+    """A generous max_context_len only adds workgroups that exit at once."""
+    w = workloads.prefill_config((20, 50), 8, 2, 64, seed=9)
+    assert_attention_close(_run(w, max_len=4096), _ref(w), "prefill max_len 4096")
+
+
+def test_prefill_out_of_pool_blocks_are_skipped(dev):
+    """With the pool bound, a prompt whose slots point past the pool reads
+    nothing out of bounds; its outputs stay finite and the others are exact."""
+    w = workloads.prefill_config((40, 24), 8, 2, 64, seed=10)
+    NB = w.key_cache.shape[0]
+    w.slot_mapping[40:] = (NB + 3) * 16 + np.arange(24) % 16   # second prompt: outside the pool
+    out = _run(w)
+    ref = _ref_first(w, 40)
+    assert_attention_close(out[:40], ref, "prefill in-pool prompt")
+    assert np.all(np.isfinite(out[40:].astype(np.float64)))
+
+
+def _ref_first(w, n):
+    return oracle.prefill_numpy(w.q[:n], w.key_cache, w.value_cache, w.slot_mapping[:n],
+                                w.context_lens[:1], w.scale)
+
+
+def test_paged_attention_prefill_op(dev):
+    """PagedAttention.prefill (paged_attention.rs:154-189): stores K/V through
+    slot_mapping, then the causal attention; query [B, S, H, D]."""
+    B, S, H, Hkv, D = 3, 37, 8, 2, 64
+    w = workloads.prefill_config((S,) * B, H, Hkv, D, seed=11, poison=True)
+    kc0 = np.full_like(w.key_cache, np.nan)
+    vc0 = np.full_like(w.value_cache, np.nan)
+    op = pa.PagedAttention(pa.PagedAttentionConfig.new(H, Hkv, D, 16))
+    kc, vc = DeviceArray.from_numpy(kc0), DeviceArray.from_numpy(vc0)
+    out = op.prefill(DeviceArray.from_numpy(w.q.reshape(B, S, H, D)),
+                     DeviceArray.from_numpy(w.key.reshape(B, S, Hkv, D)),
+                     DeviceArray.from_numpy(w.value.reshape(B, S, Hkv, D)),
+                     kc, vc, list(w.slot_mapping))
+    assert out.shape == (B, S, H, D)
+    assert_attention_close(out.numpy().reshape(B * S, H, D), _ref(w), "PagedAttention.prefill")
+    b, o = w.slot_mapping // 16, w.slot_mapping % 16
+    assert np.array_equal(kc.numpy()[b, :, :, o].view(np.uint16), w.key.view(np.uint16))
