@@ -56,6 +56,12 @@ def hip() -> ctypes.CDLL:
             "hipMemGetInfo": [ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)],
             "hipHostMalloc": [ctypes.POINTER(vp), ctypes.c_size_t, ctypes.c_uint],
             "hipHostFree": [vp],
+            "hipStreamBeginCapture": [vp, ctypes.c_int],
+            "hipStreamEndCapture": [vp, ctypes.POINTER(vp)],
+            "hipGraphInstantiate": [ctypes.POINTER(vp), vp, vp, vp, ctypes.c_size_t],
+            "hipGraphLaunch": [vp, vp],
+            "hipGraphExecDestroy": [vp],
+            "hipGraphDestroy": [vp],
         }.items():
             fn = getattr(h, name)
             fn.restype = ctypes.c_int
@@ -193,6 +199,43 @@ class Stream:
         try:
             if self.handle:
                 hip().hipStreamDestroy(self.handle)
+        except Exception:
+            pass
+
+
+class Graph:
+    """A HIP graph of the work that `enqueue()` puts on `stream`, captured
+    once and replayed with launch(). Buffers must exist before the capture:
+    allocation and synchronous copies cannot be captured."""
+
+    _CAPTURE_THREAD_LOCAL = 1
+
+    def __init__(self, stream: Stream, enqueue) -> None:
+        h = hip()
+        check(h.hipStreamBeginCapture(stream.handle, self._CAPTURE_THREAD_LOCAL),
+              "hipStreamBeginCapture")
+        g = ctypes.c_void_p()
+        try:
+            enqueue()
+        finally:
+            end = h.hipStreamEndCapture(stream.handle, ctypes.byref(g))
+        check(end, "hipStreamEndCapture")
+        self._graph = g.value
+        ex = ctypes.c_void_p()
+        check(h.hipGraphInstantiate(ctypes.byref(ex), self._graph, None, None, 0),
+              "hipGraphInstantiate")
+        self._exec = ex.value
+        self._hip = h
+
+    def launch(self, stream: Stream) -> None:
+        check(self._hip.hipGraphLaunch(self._exec, stream.handle), "hipGraphLaunch")
+
+    def __del__(self):
+        try:
+            if getattr(self, "_exec", None):
+                self._hip.hipGraphExecDestroy(self._exec)
+            if getattr(self, "_graph", None):
+                self._hip.hipGraphDestroy(self._graph)
         except Exception:
             pass
 
