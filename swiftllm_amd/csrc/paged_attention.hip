@@ -64,6 +64,7 @@ struct DecodeArgs {
     int num_blocks;   // bound on block ids; <= 0: unbounded
     int part_blocks;  // blocks per partition; 0: single pass
     int MP;           // partitions per sequence in the workspace
+    int S;            // sequences
     int snake;        // > 0: single-pass item order in snake rounds of this many
 };
 
@@ -141,41 +142,19 @@ __device__ __forceinline__ int sequence_for_block(const int* ctx, int S, int r) 
     return s_seq;
 }
 
-// At least two waves per SIMD: caps the registers (at 157 VGPRs for D=128 the
-// kernel fits three waves per SIMD), so several workgroups share a CU.
+// One (sequence, kv head, head chunk, partition) item. The NW waves of the
+// workgroup take the item's blocks round-robin and merge through LDS; the
+// result is the output (single pass, or a sequence with one partition) or a
+// split-K partial. Every thread of the workgroup calls it with the same item.
 template <int D, int NW>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
-void paged_decode_kernel(const DecodeArgs a) {
+__device__ __forceinline__ void decode_item(const DecodeArgs& a, int s, int kvh, int hc,
+                                            int part) {
     constexpr int NJ = D / 16;
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15;   // MFMA column / row-in-slice index
     const int kg = lane >> 4;  // MFMA k-group: 4 consecutive k per lane
 
-    const int part = blockIdx.x;
-    int kvh, hc, s;
-    if (a.snake > 0) {
-        // Single pass, whole grid resident: workgroup i takes item
-        // snake(i) of the longest-first list of (sequence, kv head, head
-        // chunk) items, where the list is cut into rounds of `snake`
-        // items and every other round runs backwards. Workgroups i and
-        // i + snake, which the dispatcher puts on the same CU, then pair a
-        // long sequence with a short one.
-        const int HC = gridDim.y;
-        const int i = blockIdx.z * HC + blockIdx.y;
-        const int k = i / a.snake;
-        const int pos = i - k * a.snake;
-        const int rlen = min(a.snake, static_cast<int>(gridDim.z) * HC - k * a.snake);
-        const int item = k * a.snake + ((k & 1) ? (rlen - 1 - pos) : pos);
-        const int sub = item % HC;
-        kvh = sub / a.nhc;
-        hc = sub - kvh * a.nhc;
-        s = sequence_for_block(a.ctx, gridDim.z, item / HC);
-    } else {
-        kvh = blockIdx.y / a.nhc;
-        hc = blockIdx.y - kvh * a.nhc;
-        s = sequence_for_block(a.ctx, gridDim.z, blockIdx.z);
-    }
     const int g0 = hc * 16;
     const int gn = min(16, a.G - g0);  // query heads served here
     const int gstride = min(16, a.G);  // LDS rows per wave
@@ -286,6 +265,107 @@ void paged_decode_kernel(const DecodeArgs a) {
                 a.ws_sum[pi] = den;
             }
         }
+    }
+}
+
+
+// At least two waves per SIMD: caps the registers (at 157 VGPRs for D=128 the
+// kernel fits three waves per SIMD), so several workgroups share a CU.
+template <int D, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void paged_decode_kernel(const DecodeArgs a) {
+    int kvh, hc, s;
+    if (a.snake > 0) {
+        // Single pass, whole grid resident: workgroup i takes item
+        // snake(i) of the longest-first list of (sequence, kv head, head
+        // chunk) items, where the list is cut into rounds of `snake`
+        // items and every other round runs backwards. Workgroups i and
+        // i + snake, which the dispatcher puts on the same CU, then pair a
+        // long sequence with a short one.
+        const int HC = gridDim.y;
+        const int i = blockIdx.z * HC + blockIdx.y;
+        const int k = i / a.snake;
+        const int pos = i - k * a.snake;
+        const int rlen = min(a.snake, static_cast<int>(gridDim.z) * HC - k * a.snake);
+        const int item = k * a.snake + ((k & 1) ? (rlen - 1 - pos) : pos);
+        const int sub = item % HC;
+        kvh = sub / a.nhc;
+        hc = sub - kvh * a.nhc;
+        s = sequence_for_block(a.ctx, gridDim.z, item / HC);
+    } else {
+        kvh = blockIdx.y / a.nhc;
+        hc = blockIdx.y - kvh * a.nhc;
+        s = sequence_for_block(a.ctx, gridDim.z, blockIdx.z);
+    }
+    decode_item<D, NW>(a, s, kvh, hc, 0);
+}
+
+// Split-K partitions. The items are the real (sequence, partition) pairs
+// times the kv-head chunks: every workgroup builds the prefix of partitions
+// per sequence in LDS and walks items blockIdx.x, + gridDim.x, ... The grid
+// is sized to the resident workgroups, not to the worst case of every
+// sequence, so a ragged batch launches no empty workgroups (a grid over
+// max_num_blocks_per_seq would be mostly empty). Batches of more than
+// kPartMaxSeqs sequences take one item per workgroup over the full grid.
+constexpr int kPartMaxSeqs = 4096;
+
+template <int D, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void paged_partition_kernel(const DecodeArgs a) {
+    const int HC = a.Hkv * a.nhc;
+    if (a.S > kPartMaxSeqs) {
+        const int it = blockIdx.x;
+        const int part = it % a.MP;
+        const int sub = (it / a.MP) % HC;
+        const int s = it / (a.MP * HC);
+        if (s < a.S) decode_item<D, NW>(a, s, sub / a.nhc, sub % a.nhc, part);
+        return;
+    }
+    __shared__ int s_pre[kPartMaxSeqs + 1];
+    __shared__ int s_wave[NW];
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    // Partitions per sequence (at least one: an empty sequence's item
+    // writes its zeros), exclusive prefix in chunks of the workgroup.
+    int carry = 0;
+    for (int c0 = 0; c0 < a.S; c0 += NW * 64) {
+        const int sq = c0 + static_cast<int>(threadIdx.x);
+        int v = 0;
+        if (sq < a.S) {
+            const int L = max(a.ctx[sq], 0);
+            const int nblk = min((L + kBlockTokens - 1) / kBlockTokens, a.MB);
+            v = max((nblk + a.part_blocks - 1) / a.part_blocks, 1);
+        }
+        int x = v;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int y = __shfl_up(x, d);
+            if (lane >= d) x += y;
+        }
+        if (lane == 63) s_wave[w] = x;
+        __syncthreads();
+        int before = carry, chunk = 0;
+        for (int i = 0; i < NW; ++i) {
+            before += (i < w) ? s_wave[i] : 0;
+            chunk += s_wave[i];
+        }
+        if (sq < a.S) s_pre[sq] = before + x - v;
+        carry += chunk;
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) s_pre[a.S] = carry;
+    __syncthreads();
+    const int total = carry * HC;
+    for (int it = blockIdx.x; it < total; it += gridDim.x) {
+        const int pidx = it / HC;
+        const int sub = it - pidx * HC;
+        int lo = 0, hi = a.S;  // s_pre[lo] <= pidx < s_pre[hi]
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (s_pre[mid] <= pidx) lo = mid; else hi = mid;
+        }
+        decode_item<D, NW>(a, lo, sub / a.nhc, sub % a.nhc, pidx - s_pre[lo]);
+        __syncthreads();  // the item's LDS is free again
     }
 }
 
@@ -865,6 +945,31 @@ hipError_t launch_decode(const DecodeArgs& a, int D, int S, int mp_grid, hipStre
                     : launch_decode_t<64, NW>(a, S, mp_grid, stream);
 }
 
+template <int D, int NW>
+hipError_t launch_partition_t(const DecodeArgs& a, unsigned grid, hipStream_t stream) {
+    const int gstride = a.G < 16 ? a.G : 16;
+    const size_t lds = static_cast<size_t>(NW) * 32 * sizeof(float) +
+                       static_cast<size_t>(NW) * gstride * D * sizeof(float);
+    return launch(paged_partition_kernel<D, NW>, dim3(grid), dim3(NW * 64), lds, stream, a);
+}
+
+int device_cus();
+
+// Split-K partition kernel: a grid of resident workgroups (three 4-wave
+// workgroups per CU, four rounds) walking the compacted item list, or one
+// workgroup per possible item for batches too large to compact in LDS.
+template <int NW>
+hipError_t launch_partition(const DecodeArgs& a, int D, hipStream_t stream, bool* too_large) {
+    const long long possible = static_cast<long long>(a.MP) * a.Hkv * a.nhc * a.S;
+    long long grid = possible;
+    if (a.S <= kPartMaxSeqs) grid = std::min(possible, 12LL * device_cus());
+    *too_large = grid > 0x7fffffffLL;
+    if (*too_large || grid <= 0) return hipSuccess;
+    const unsigned g = static_cast<unsigned>(grid);
+    return D == 128 ? launch_partition_t<128, NW>(a, g, stream)
+                    : launch_partition_t<64, NW>(a, g, stream);
+}
+
 DecodeArgs make_args(void* out, const void* q, const void* kc, const void* vc, const int* bt,
                      const int* ctx, float scale, const Shape& sh, int num_blocks) {
     DecodeArgs a{};
@@ -880,11 +985,11 @@ DecodeArgs make_args(void* out, const void* q, const void* kc, const void* vc, c
     a.G = sh.H / sh.Hkv;
     a.nhc = (a.G + 15) / 16;
     a.MB = sh.MB;
+    a.S = sh.S;
     a.num_blocks = num_blocks;
     return a;
 }
 
-int device_cus();
 
 int decode_v1(void* out, const void* q, const void* kc, const void* vc, const int* bt,
               const int* ctx, float scale, const Shape& sh, int num_blocks, hipStream_t stream,
@@ -1059,7 +1164,12 @@ int decode_v2(void* out, void* ws, size_t ws_bytes, const void* q, const void* k
     a.ws_out = reinterpret_cast<float*>(base + 2 * need.stat);
     a.part_blocks = partition_size / kBlockTokens;
     a.MP = need.MP;
-    hipError_t err = launch_decode<kWavesV2>(a, sh.D, sh.S, need.MP, stream);
+    bool too_large = false;
+    hipError_t err = launch_partition<kWavesV2>(a, sh.D, stream, &too_large);
+    if (too_large) {
+        return fail(SWIFTLLM_ERR_NOT_SUPPORTED, "%s: %d sequences x %d partitions is too many",
+                    who, sh.S, need.MP);
+    }
     if (err != hipSuccess || need.MP <= 1) return launched(err, who);
     ReduceArgs r{};
     r.out = a.out;
