@@ -262,3 +262,58 @@ def test_paged_attention_op(dev):
     assert_attention_close(out[:, 0], ref, "PagedAttention.decode")
     with pytest.raises(pa.InvalidParameter):
         op.reshape_and_cache(DeviceArray.from_numpy(k), DeviceArray.from_numpy(v), kc_d, vc_d, slots[:-1])
+
+
+def test_pool_past_two_gigaelements(dev):
+    """A pool of 140,000 blocks (4.6 GB per cache at Hkv 8, D 128): element
+    offsets pass 2^31, where the reference's int arithmetic (cu:86) wraps.
+    Block tables point at the highest blocks; the K/V get there through
+    reshape_and_cache on the device, and the decode must match the oracle on
+    a compact relabelled copy of the same blocks, for every entry point."""
+    S, H, Hkv, D, NB = 4, 32, 8, 128, 140_000
+    ctx = np.array([1, 40, 129, 300], np.int32)
+    nblk = (ctx + 15) // 16
+    MB = int(nblk.max())
+    rng = np.random.default_rng(41)
+    high = NB - 1 - rng.permutation(2000)[: int(nblk.sum())]     # ids 138,000 .. 139,999
+    bt = np.zeros((S, MB), np.int32)
+    slots, keys, vals, pos = [], [], [], 0
+    for s in range(S):
+        bt[s, : nblk[s]] = high[pos: pos + nblk[s]]
+        pos += nblk[s]
+        for p in range(ctx[s]):
+            slots.append(int(bt[s, p // 16]) * 16 + p % 16)
+    T = len(slots)
+    key = rng.standard_normal((T, Hkv, D)).astype(np.float16)
+    value = rng.standard_normal((T, Hkv, D)).astype(np.float16)
+    kc, vc = DeviceArray((NB, Hkv, D, 16), np.float16), DeviceArray((NB, Hkv, D, 16), np.float16)
+    assert kc.nbytes > 2 ** 32
+    pa.launch_reshape_and_cache(DeviceArray.from_numpy(key), DeviceArray.from_numpy(value), kc, vc,
+                                DeviceArray.from_numpy(np.array(slots, np.int32)), T, Hkv, D, 16,
+                                num_blocks=NB)
+    # compact host copy: the used blocks relabelled 0..n-1
+    used = np.unique(bt[bt > 0]) if (bt > 0).any() else np.array([], np.int64)
+    relabel = {int(b): i for i, b in enumerate(used)}
+    kc_h = np.zeros((len(used), Hkv, D, 16), np.float16)
+    vc_h = np.zeros_like(kc_h)
+    sl = np.array(slots)
+    rb = np.array([relabel[int(x)] for x in sl // 16])
+    kc_h[rb, :, :, sl % 16] = key
+    vc_h[rb, :, :, sl % 16] = value
+    bt_h = np.vectorize(lambda b: relabel.get(int(b), 0))(bt).astype(np.int32)
+    q = rng.standard_normal((S, H, D)).astype(np.float16)
+    scale = 1.0 / np.sqrt(D)
+    ref = oracle.decode_f64(q, kc_h, vc_h, bt_h, ctx, scale)
+    qd, btd, cd = DeviceArray.from_numpy(q), DeviceArray.from_numpy(bt), DeviceArray.from_numpy(ctx)
+    out = DeviceArray((S, H, D), np.float16)
+    pa.paged_attention_v1(out, qd, kc, vc, btd, cd, scale, S, H, Hkv, D, 16, MB, num_blocks=NB)
+    synchronize()
+    assert_attention_close(out.numpy(), ref, "v1 on a 140k-block pool")
+    for ps in (32, 0):
+        ws = pa.workspace(pa.paged_attention_v2_workspace_size(S, H, Hkv, D, 16, MB, ps))
+        pa.paged_attention_v2(out, ws, qd, kc, vc, btd, cd, scale, S, H, Hkv, D, 16, MB, ps,
+                              num_blocks=NB)
+        synchronize()
+        assert_attention_close(out.numpy(), ref, f"v2 ps={ps} on a 140k-block pool")
+    kc.free()
+    vc.free()
