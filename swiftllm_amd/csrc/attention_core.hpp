@@ -16,6 +16,17 @@ __device__ __forceinline__ f4 mfma16(h4 a, h4 b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
 
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+// gfx950's full-rate 16 x 16 x 32 form: lane (m, q) holds k = 8q .. 8q + 7.
+__device__ __forceinline__ f4 mfma16x32(h8 a, h8 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ h8 cat8(h4 lo, h4 hi) {
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
 __device__ __forceinline__ h4 mask_h4(h4 v, unsigned long long m) {
     return __builtin_bit_cast(h4, __builtin_bit_cast(unsigned long long, v) & m);
 }
@@ -96,15 +107,12 @@ struct WaveState {
 // The first nv tokens of the tile exist (the rest is zeroed so stale values
 // cannot reach a sum; nv == 0: the block contributes nothing), and query row
 // g = lane % 16 of this lane sees tokens t < lim (lim <= nv).
+// Zeroes the K/V of tokens nv.. of the tile (tail block) so no stale value
+// (possibly NaN) reaches a sum through a 0 weight.
 template <int D>
-__device__ __forceinline__ void attend_block(WaveState<D>& st, int nv, int lim, int kg,
-                                             h4 (&kA)[D / 16], h4 (&vA)[D / 16],
-                                             const QOperand<D>& qB, h4 ident,
-                                             float scale_log2) {
+__device__ __forceinline__ void mask_tail(int nv, int kg, h4 (&kA)[D / 16], h4 (&vA)[D / 16]) {
     constexpr int NJ = D / 16;
     if (nv < kBlockTokens) {
-        // Tail block: zero the K/V of tokens past the context so no stale
-        // value (possibly NaN) reaches a sum through a 0 weight.
         const int c = min(max(nv - 4 * kg, 0), 4);
         const unsigned long long m = (c >= 4) ? ~0ull : ((1ull << (16 * c)) - 1ull);
 #pragma unroll
@@ -113,19 +121,14 @@ __device__ __forceinline__ void attend_block(WaveState<D>& st, int nv, int lim, 
             vA[J] = mask_h4(vA[J], m);
         }
     }
-    // Steps 1 + 2.
-    f4 s0 = f4{0, 0, 0, 0}, s1 = f4{0, 0, 0, 0};
-#pragma unroll
-    for (int J = 0; J < NJ; ++J) {
-        const f4 t = mfma16(kA[J], ident, f4{0, 0, 0, 0});
-        const h4 kT = to_h4(t);
-        if (J & 1) {
-            s1 = mfma16(kT, qB.get(J), s1);
-        } else {
-            s0 = mfma16(kT, qB.get(J), s0);
-        }
-    }
-    // Step 3. Lane (r, kg) holds S^T[t = 4kg + i][g = r].
+}
+
+// Steps 3 + 4 for one group of 16 query rows, from the two halves s0 + s1
+// of the S^T accumulator. Lane (r, kg) holds S^T[t = 4kg + i][g = r].
+template <int D>
+__device__ __forceinline__ void softmax_pv(WaveState<D>& st, f4 s0, f4 s1, int lim, int kg,
+                                           const h4 (&vA)[D / 16], float scale_log2) {
+    constexpr int NJ = D / 16;
     float sv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -162,6 +165,59 @@ __device__ __forceinline__ void attend_block(WaveState<D>& st, int nv, int lim, 
         st.acc[J] = mfma16(vA[J], ph, st.acc[J]);
         st.acc[J] = mfma16(vA[J], pl, st.acc[J]);
     }
+}
+
+template <int D>
+__device__ __forceinline__ void attend_block(WaveState<D>& st, int nv, int lim, int kg,
+                                             h4 (&kA)[D / 16], h4 (&vA)[D / 16],
+                                             const QOperand<D>& qB, h4 ident,
+                                             float scale_log2) {
+    constexpr int NJ = D / 16;
+    mask_tail<D>(nv, kg, kA, vA);
+    // Steps 1 + 2.
+    f4 s0 = f4{0, 0, 0, 0}, s1 = f4{0, 0, 0, 0};
+#pragma unroll
+    for (int J = 0; J < NJ; ++J) {
+        const f4 t = mfma16(kA[J], ident, f4{0, 0, 0, 0});
+        const h4 kT = to_h4(t);
+        if (J & 1) {
+            s1 = mfma16(kT, qB.get(J), s1);
+        } else {
+            s0 = mfma16(kT, qB.get(J), s0);
+        }
+    }
+    softmax_pv<D>(st, s0, s1, lim, kg, vA, scale_log2);
+}
+
+// The same block for two groups of 16 query rows that share the kv head:
+// the K tile is transposed once and feeds both QK^T products. QK^T runs on
+// the 16x16x32 form over pairs of 16-row slices (J0 = 2J', J1 = 2J' + 1):
+// with k = 8q + i read as d = 16 J0 + 4q + i for i < 4 and 16 J1 + 4q + i - 4
+// otherwise, the A operand is the lane's two transposed slices side by side
+// and the B operand its two Q pieces side by side.
+template <int D>
+__device__ __forceinline__ void attend_block_pair(WaveState<D>& sa, WaveState<D>& sb, int nv,
+                                                  int lim_a, int lim_b, int kg,
+                                                  h4 (&kA)[D / 16], h4 (&vA)[D / 16],
+                                                  const QOperand<D>& qa, const QOperand<D>& qb,
+                                                  h4 ident, float scale_log2) {
+    constexpr int NJ = D / 16;
+    mask_tail<D>(nv, kg, kA, vA);
+    f4 a0 = f4{0, 0, 0, 0}, a1 = f4{0, 0, 0, 0}, b0 = f4{0, 0, 0, 0}, b1 = f4{0, 0, 0, 0};
+#pragma unroll
+    for (int J = 0; J < NJ; J += 2) {
+        const h8 kT = cat8(to_h4(mfma16(kA[J], ident, f4{0, 0, 0, 0})),
+                           to_h4(mfma16(kA[J + 1], ident, f4{0, 0, 0, 0})));
+        if (J & 2) {
+            a1 = mfma16x32(kT, cat8(qa.get(J), qa.get(J + 1)), a1);
+            b1 = mfma16x32(kT, cat8(qb.get(J), qb.get(J + 1)), b1);
+        } else {
+            a0 = mfma16x32(kT, cat8(qa.get(J), qa.get(J + 1)), a0);
+            b0 = mfma16x32(kT, cat8(qb.get(J), qb.get(J + 1)), b0);
+        }
+    }
+    softmax_pv<D>(sa, a0, a1, lim_a, kg, vA, scale_log2);
+    softmax_pv<D>(sb, b0, b1, lim_b, kg, vA, scale_log2);
 }
 
 // Every query row sees the same nv tokens (decode).

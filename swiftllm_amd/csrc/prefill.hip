@@ -15,12 +15,14 @@
 // (slot of p = table[p / 16] * 16 + p % 16, what get_slot_mapping produces):
 // the kernel reads the block of 16 positions from the slot of the first.
 //
-// Work decomposition. A wave owns 16 MFMA query rows: tpw = 16 / gw
-// consecutive query tokens times gw = min(G, 16) query heads of one kv head,
-// so every K/V tile it loads serves all of them. It walks the key blocks up
-// to its last token with the decode kernel's per-block MFMA step; each lane's
-// query row carries its own causal limit. A wave's rows are complete when its
-// walk ends, so it writes its outputs directly: no combine, no barriers.
+// Work decomposition. A wave owns two groups of 16 MFMA query rows; a group
+// is tpw = 16 / gw consecutive query tokens times gw = min(G, 16) query heads
+// of one kv head, and the second group takes the next tpw tokens. Every K/V
+// tile the wave loads serves both groups, and the K tile is transposed once
+// for both. The wave walks the key blocks up to its last token with the
+// decode kernel's per-block MFMA step; each lane's query row carries its own
+// causal limit. A wave's rows are complete when its walk ends, so it writes
+// its outputs directly: no combine, no barriers.
 // Four waves per workgroup take consecutive token groups; workgroups go out
 // latest tokens first (the longest walks start first). K/V tiles are loaded
 // with ordinary (cached) loads: every query group of a sequence re-reads them.
@@ -48,7 +50,7 @@ struct PrefillArgs {
     int G;               // query heads per kv head
     int nhc;             // head chunks of 16 per kv head
     int gw;              // query heads per row group: min(G, 16)
-    int tpw;             // query tokens per wave: 16 / gw
+    int tpw;             // query tokens per row group: 16 / gw (a wave has two groups)
     int groups;          // workgroups per (sequence, kv head chunk) in the grid
     int num_blocks;      // bound on block ids; <= 0: unbounded
 };
@@ -79,26 +81,34 @@ void paged_prefill_kernel(const PrefillArgs a) {
     for (int i = 0; i < kPrefillWaves; ++i) start += s_part[i];
     const int L = max(a.ctx[s], 0);
 
-    const int tq0 = (gi * kPrefillWaves + w) * a.tpw;  // first query token of this wave
+    // The wave's two groups of 16 query rows: tokens tq0 .. tq0 + tpw - 1
+    // (group a) and the next tpw (group b).
+    const int tq0 = (gi * kPrefillWaves + w) * 2 * a.tpw;
     if (tq0 >= L) return;
-    const int tq_last = min(tq0 + a.tpw, L) - 1;
+    const int tq_last = min(tq0 + 2 * a.tpw, L) - 1;
 
-    // Query row r: token tq0 + r / gw, head h0 + r % gw.
+    // Query row r of group k: token tq0 + k * tpw + r / gw, head h0 + r % gw.
     const int rt = r / a.gw;
     const int rh = r - rt * a.gw;
     const int g = hc * 16 + rh;
-    const int tq = tq0 + rt;
-    const bool row_ok = (rt < a.tpw) && (tq < L) && (g < a.G);
     const int h = kvh * a.G + min(g, a.G - 1);
-    const size_t qrow = (static_cast<size_t>(start) + min(tq, L - 1)) * a.H + h;
+    const int tqa = tq0 + rt;
+    const int tqb = tq0 + a.tpw + rt;
+    const bool ok_a = (rt < a.tpw) && (tqa < L) && (g < a.G);
+    const bool ok_b = (rt < a.tpw) && (tqb < L) && (g < a.G);
+    const size_t qrow_a = (static_cast<size_t>(start) + min(tqa, L - 1)) * a.H + h;
+    const size_t qrow_b = (static_cast<size_t>(start) + min(tqb, L - 1)) * a.H + h;
 
-    QOperand<D> qB;
+    QOperand<D> qa, qb;
     {
-        const f16* qp = a.q + qrow * D + 4 * kg;
+        const f16* pa_ = a.q + qrow_a * D + 4 * kg;
+        const f16* pb_ = a.q + qrow_b * D + 4 * kg;
 #pragma unroll
         for (int J = 0; J < NJ; ++J) {
-            const h4 v = *reinterpret_cast<const h4*>(qp + 16 * J);
-            qB.v[J] = row_ok ? v : h4{0, 0, 0, 0};
+            const h4 va = *reinterpret_cast<const h4*>(pa_ + 16 * J);
+            const h4 vb = *reinterpret_cast<const h4*>(pb_ + 16 * J);
+            qa.v[J] = ok_a ? va : h4{0, 0, 0, 0};
+            qb.v[J] = ok_b ? vb : h4{0, 0, 0, 0};
         }
     }
     h4 ident;
@@ -109,11 +119,11 @@ void paged_prefill_kernel(const PrefillArgs a) {
     const int loff = kv_elem_offset(r, 4 * kg);
     const const_int* srow = as_const(a.slots) + start;
 
-    WaveState<D> st;
-    st.m = -INFINITY;
-    st.l = 0.0f;
+    WaveState<D> sa, sb;
+    sa.m = sb.m = -INFINITY;
+    sa.l = sb.l = 0.0f;
 #pragma unroll
-    for (int J = 0; J < NJ; ++J) st.acc[J] = f4{0, 0, 0, 0};
+    for (int J = 0; J < NJ; ++J) sa.acc[J] = sb.acc[J] = f4{0, 0, 0, 0};
 
     // Key blocks 0 .. nkb-1, double-buffered like the decode walk: the
     // steady loop runs while at least three blocks are left (both loads of
@@ -126,8 +136,9 @@ void paged_prefill_kernel(const PrefillArgs a) {
     auto attend = [&](int jb, int b, h4 (&k)[NJ], h4 (&v)[NJ]) {
         const int base = jb * kBlockTokens;
         const int nv = block_ok(b, a.num_blocks) ? min(kBlockTokens, L - base) : 0;
-        const int lim = row_ok ? min(max(tq + 1 - base, 0), nv) : 0;
-        attend_block<D>(st, nv, lim, kg, k, v, qB, ident, a.scale_log2);
+        const int lim_a = ok_a ? min(max(tqa + 1 - base, 0), nv) : 0;
+        const int lim_b = ok_b ? min(max(tqb + 1 - base, 0), nv) : 0;
+        attend_block_pair<D>(sa, sb, nv, lim_a, lim_b, kg, k, v, qa, qb, ident, a.scale_log2);
     };
     {
         h4 kA[NJ], vA[NJ], kB[NJ], vB[NJ];
@@ -156,19 +167,23 @@ void paged_prefill_kernel(const PrefillArgs a) {
         }
     }
 
-    float l_run = st.l;
-    l_run += __shfl_xor(l_run, 16);
-    l_run += __shfl_xor(l_run, 32);
-    if (!row_ok) return;
-    const float inv = (l_run > 0.0f) ? 1.0f / l_run : 0.0f;
-    f16* op = a.out + qrow * D + 4 * kg;
+    auto store = [&](const WaveState<D>& st, bool ok, size_t qrow) {
+        float l_run = st.l;
+        l_run += __shfl_xor(l_run, 16);
+        l_run += __shfl_xor(l_run, 32);
+        if (!ok) return;
+        const float inv = (l_run > 0.0f) ? 1.0f / l_run : 0.0f;
+        f16* op = a.out + qrow * D + 4 * kg;
 #pragma unroll
-    for (int J = 0; J < NJ; ++J) {
-        h4 o;
+        for (int J = 0; J < NJ; ++J) {
+            h4 o;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = static_cast<f16>(st.acc[J][i] * inv);
-        *reinterpret_cast<h4*>(op + 16 * J) = o;
-    }
+            for (int i = 0; i < 4; ++i) o[i] = static_cast<f16>(st.acc[J][i] * inv);
+            *reinterpret_cast<h4*>(op + 16 * J) = o;
+        }
+    };
+    store(sa, ok_a, qrow_a);
+    store(sb, ok_b, qrow_b);
 }
 
 int prefill(const char* who, void* out, const void* q, const void* kc, const void* vc,
@@ -216,7 +231,7 @@ int prefill(const char* who, void* out, const void* q, const void* kc, const voi
     a.nhc = (a.G + 15) / 16;
     a.gw = a.G < 16 ? a.G : 16;
     a.tpw = 16 / a.gw;
-    const long long per_wg = static_cast<long long>(kPrefillWaves) * a.tpw;
+    const long long per_wg = static_cast<long long>(kPrefillWaves) * 2 * a.tpw;
     a.groups = static_cast<int>((max_len + per_wg - 1) / per_wg);
     a.num_blocks = num_blocks;
     const dim3 grid(static_cast<unsigned>(a.groups), static_cast<unsigned>(a.Hkv * a.nhc),
