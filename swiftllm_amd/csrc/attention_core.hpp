@@ -125,7 +125,10 @@ __device__ __forceinline__ void mask_tail(int nv, int kg, h4 (&kA)[D / 16], h4 (
 
 // Steps 3 + 4 for one group of 16 query rows, from the two halves s0 + s1
 // of the S^T accumulator. Lane (r, kg) holds S^T[t = 4kg + i][g = r].
-template <int D>
+// PV32 runs PV on the 16x16x32 form: k = 8q + i is token 4q + i of the hi
+// half of P for i < 4 and of the lo half otherwise, so the A operand is the
+// lane's V piece twice and the B operand its hi and lo pieces side by side.
+template <int D, bool PV32 = false>
 __device__ __forceinline__ void softmax_pv(WaveState<D>& st, f4 s0, f4 s1, int lim, int kg,
                                            const h4 (&vA)[D / 16], float scale_log2) {
     constexpr int NJ = D / 16;
@@ -160,10 +163,16 @@ __device__ __forceinline__ void softmax_pv(WaveState<D>& st, f4 s0, f4 s1, int l
         pl[i] = static_cast<f16>(p[i] - static_cast<float>(ph[i]));
     }
     // Step 4. Lane (r, kg) accumulates O^T[d = 16J + 4kg + i][g = r].
+    if constexpr (PV32) {
+        const h8 p8 = cat8(ph, pl);
 #pragma unroll
-    for (int J = 0; J < NJ; ++J) {
-        st.acc[J] = mfma16(vA[J], ph, st.acc[J]);
-        st.acc[J] = mfma16(vA[J], pl, st.acc[J]);
+        for (int J = 0; J < NJ; ++J) st.acc[J] = mfma16x32(cat8(vA[J], vA[J]), p8, st.acc[J]);
+    } else {
+#pragma unroll
+        for (int J = 0; J < NJ; ++J) {
+            st.acc[J] = mfma16(vA[J], ph, st.acc[J]);
+            st.acc[J] = mfma16(vA[J], pl, st.acc[J]);
+        }
     }
 }
 
@@ -216,8 +225,8 @@ __device__ __forceinline__ void attend_block_pair(WaveState<D>& sa, WaveState<D>
             b0 = mfma16x32(kT, cat8(qb.get(J), qb.get(J + 1)), b0);
         }
     }
-    softmax_pv<D>(sa, a0, a1, lim_a, kg, vA, scale_log2);
-    softmax_pv<D>(sb, b0, b1, lim_b, kg, vA, scale_log2);
+    softmax_pv<D, true>(sa, a0, a1, lim_a, kg, vA, scale_log2);
+    softmax_pv<D, true>(sb, b0, b1, lim_b, kg, vA, scale_log2);
 }
 
 // Every query row sees the same nv tokens (decode).
