@@ -369,97 +369,86 @@ void paged_partition_kernel(const DecodeArgs a) {
     }
 }
 
-// Rescaled combine of P fragments (max m_p, sum l_p, normalised partial
-// o_p[d]) for gn <= 16 heads into out[g][d] = sum_p w_p o_p / sum_p w_p with
-// w_p = exp2(m_p - M) l_p. Fragment accessors: fm(p, g), fl(p, g) and
-// fo(p, g) (pointer to o_p of head g, 16-byte aligned). Runs on
-// kCombineThreads threads: the per-head max and denominator are reduced
-// across the workgroup, the weights go through LDS in chunks, and each
-// thread owns 4 consecutive outputs (one 16-byte load per fragment) of a
-// 1/F share of the fragments, F = threads / (gn * D / 4); an LDS pass adds
-// the F shares. The loads of a thread are independent, so many are in
-// flight at once.
-constexpr int kCombineThreads = 1024;
-constexpr int kCombineChunk = 256;
+// Rescaled combine of P fragments of one query head: fragment p holds a max
+// m_p (log2 domain), a sum l_p and a normalised partial output o_p[D], and
+// out[d] = sum_p w_p o_p[d] / sum_p w_p with w_p = exp2(m_p - M) l_p,
+// M = max_p m_p. One workgroup of kReduceThreads threads per head: threads
+// own 4 consecutive outputs (one 16-byte load per fragment) of every PG-th
+// fragment, so PG fragments are in flight per load step, and an LDS pass adds
+// the PG shares. Accessors: fm(p), fl(p) and fo(p) (pointer to o_p, 16-byte
+// aligned); out(d, v) stores one output.
+constexpr int kReduceThreads = 256;
+constexpr int kReduceChunk = 1024;  // fragment weights staged in LDS per pass
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
 
 template <int D, typename FM, typename FL, typename FO, typename OUT>
-__device__ __forceinline__ void combine_fragments(int P, int gn, FM fm, FL fl, FO fo, OUT out) {
-    constexpr int kWaves = kCombineThreads / 64;
-    __shared__ float s_red[16][kWaves];
-    __shared__ float s_M[16];
-    __shared__ float s_den[16];
-    __shared__ float s_w[16][kCombineChunk];
-    __shared__ f4 s_part[kCombineThreads];
+__device__ __forceinline__ void combine_head(int P, FM fm, FL fl, FO fo, OUT out) {
+    constexpr int LQ = D / 4;                 // threads per fragment row
+    constexpr int PG = kReduceThreads / LQ;   // fragment shares
+    constexpr int NWV = kReduceThreads / 64;
+    __shared__ float s_w[kReduceChunk];
+    __shared__ float s_red[2][NWV];
+    __shared__ f4 s_acc[kReduceThreads];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wv = tid >> 6;
-    for (int g = 0; g < gn; ++g) {
-        float m = -INFINITY;
-        for (int p = tid; p < P; p += kCombineThreads) m = fmaxf(m, fm(p, g));
-        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-        if (lane == 0) s_red[g][wv] = m;
-    }
+    float m = -INFINITY;
+    for (int p = tid; p < P; p += kReduceThreads) m = fmaxf(m, fm(p));
+    m = wave_max(m);
+    if (lane == 0) s_red[0][wv] = m;
     __syncthreads();
-    if (tid < gn) {
-        float m = -INFINITY;
-        for (int i = 0; i < kWaves; ++i) m = fmaxf(m, s_red[tid][i]);
-        s_M[tid] = m;
-    }
-    __syncthreads();
-    for (int g = 0; g < gn; ++g) {
-        const float M = s_M[g];
-        float d = 0.0f;
-        for (int p = tid; p < P; p += kCombineThreads) {
-            const float mp = fm(p, g);
-            d += (mp == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mp - M) * fl(p, g);
-        }
-        for (int off = 32; off > 0; off >>= 1) d += __shfl_xor(d, off);
-        if (lane == 0) s_red[g][wv] = d;
-    }
-    __syncthreads();
-    if (tid < gn) {
-        float d = 0.0f;
-        for (int i = 0; i < kWaves; ++i) d += s_red[tid][i];
-        s_den[tid] = d;
-    }
-    const int quads = gn * (D / 4);
-    const int F = kCombineThreads / quads;  // fragment shares (>= 2)
-    const int quad = tid % quads;
-    const int share = tid / quads;
-    const int g = quad / (D / 4);
-    const int d4 = (quad - g * (D / 4)) * 4;
-    f4 acc = f4{0, 0, 0, 0};
-    for (int c0 = 0; c0 < P; c0 += kCombineChunk) {
-        const int cn = min(kCombineChunk, P - c0);
-        __syncthreads();
-        for (int i = tid; i < gn * cn; i += kCombineThreads) {
-            const int gg = i / cn;
-            const int p = c0 + (i - gg * cn);
-            const float mp = fm(p, gg);
-            s_w[gg][p - c0] = (mp == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mp - s_M[gg]) * fl(p, gg);
-        }
-        __syncthreads();
-        if (share < F) {
-#pragma unroll 8
-            for (int p = share; p < cn; p += F) {
-                acc += s_w[g][p] * *reinterpret_cast<const f4*>(fo(c0 + p, g) + d4);
-            }
-        }
-    }
-    s_part[tid] = acc;
-    __syncthreads();
-    if (tid < quads) {
-        f4 sum = s_part[tid];
-        for (int f = 1; f < F; ++f) sum += s_part[f * quads + tid];
-        const float den = s_den[g];
-        const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+    float M = s_red[0][0];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) out(g, d4 + i, sum[i] * inv);
+    for (int i = 1; i < NWV; ++i) M = fmaxf(M, s_red[0][i]);
+    const int share = tid / LQ;
+    const int d4 = (tid - share * LQ) * 4;
+    f4 acc = f4{0, 0, 0, 0};
+    float den = 0.0f;
+    for (int c0 = 0; c0 < P; c0 += kReduceChunk) {
+        const int cn = min(kReduceChunk, P - c0);
+        for (int i = tid; i < cn; i += kReduceThreads) {
+            const float mp = fm(c0 + i);
+            const float w = (mp == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mp - M) * fl(c0 + i);
+            s_w[i] = w;
+            den += w;
+        }
+        __syncthreads();
+#pragma unroll 4
+        for (int i = share; i < cn; i += PG) {
+            acc += s_w[i] * *reinterpret_cast<const f4*>(fo(c0 + i) + d4);
+        }
+        __syncthreads();
+    }
+    den = wave_sum(den);
+    if (lane == 0) s_red[1][wv] = den;
+    s_acc[tid] = acc;
+    __syncthreads();
+    if (tid < LQ) {
+        f4 sum = s_acc[tid];
+#pragma unroll
+        for (int f = 1; f < PG; ++f) sum += s_acc[f * LQ + tid];
+        float dd = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NWV; ++i) dd += s_red[1][i];
+        const float inv = dd > 0.0f ? 1.0f / dd : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) out(d4 + i, sum[i] * inv);
     }
 }
 
-// Split-K reduce: one workgroup per (sequence, kv head, head chunk) with more
-// than one partition; partition p contributes exp2(m_p - M) * l_p * o_p.
+// Split-K reduce: one workgroup per (query head, sequence); sequences with a
+// single partition were written directly by the partition kernel.
 struct ReduceArgs {
     f16* out;
     const int* ctx;
@@ -467,32 +456,28 @@ struct ReduceArgs {
     const float* ws_sum;
     const float* ws_out;
     int H;
-    int G;
-    int nhc;
     int MB;
     int part_blocks;
     int MP;
 };
 
 template <int D>
-__global__ __launch_bounds__(kCombineThreads) void paged_reduce_kernel(const ReduceArgs a) {
-    const int kvh = blockIdx.x / a.nhc;
-    const int hc = blockIdx.x - kvh * a.nhc;
+__global__ __launch_bounds__(kReduceThreads) void paged_reduce_kernel(const ReduceArgs a) {
+    const int h = blockIdx.x;
     const int s = blockIdx.y;
-    const int g0 = hc * 16;
-    const int gn = min(16, a.G - g0);
-    const int h0 = kvh * a.G + g0;
     const int L = max(a.ctx[s], 0);
     const int nblk = min((L + kBlockTokens - 1) / kBlockTokens, a.MB);
     const int nparts = (nblk + a.part_blocks - 1) / a.part_blocks;
-    if (nparts <= 1) return;  // written directly by the partition kernel
-    const size_t hb = static_cast<size_t>(s) * a.H + h0;  // first head row of this chunk
-    combine_fragments<D>(
-        nparts, gn,
-        [&](int p, int g) { return a.ws_max[(hb + g) * a.MP + p]; },
-        [&](int p, int g) { return a.ws_sum[(hb + g) * a.MP + p]; },
-        [&](int p, int g) { return a.ws_out + ((hb + g) * a.MP + p) * D; },
-        [&](int g, int d, float v) { a.out[(hb + g) * D + d] = static_cast<f16>(v); });
+    if (nparts <= 1) return;
+    const size_t row = static_cast<size_t>(s) * a.H + h;
+    const float* pm = a.ws_max + row * a.MP;
+    const float* pl = a.ws_sum + row * a.MP;
+    const float* po = a.ws_out + row * a.MP * D;
+    f16* o = a.out + row * D;
+    combine_head<D>(
+        nparts, [&](int p) { return pm[p]; }, [&](int p) { return pl[p]; },
+        [&](int p) { return po + static_cast<size_t>(p) * D; },
+        [&](int d, float v) { o[d] = static_cast<f16>(v); });
 }
 
 // ---------------------------------------------------------------------------
@@ -702,12 +687,12 @@ void paged_decode_streamk_kernel(const StreamArgs a) {
     }
 }
 
-// Combines the fragments of every split item, one wave per wave of the main
-// grid: wave w reduces the item of its first segment when that segment is
-// split, starts inside the sequence, and w's team is the first team to start
-// inside it (every other wave exits at once). Fragments of the item come from
-// the waves with the same team member index in teams ta..tb; there are few of
-// them (a sequence spans ceil(blocks / q) + 1 teams at most).
+// Combines the fragments of every split item: workgroup (w, g) reduces query
+// head g of the item whose fragments wave w owns. Wave w owns the item of its
+// first segment when that segment is split, starts inside the sequence, and
+// w's team is the first team to start inside it (every other workgroup exits
+// at once). Fragments of the item come from the waves with the same team
+// member index in teams ta..tb.
 struct StreamReduceArgs {
     f16* out;
     const float* frag;
@@ -716,19 +701,10 @@ struct StreamReduceArgs {
     int gstride;
 };
 
-// Fragments per item the wave-level reduce keeps in LDS; items split over
-// more teams are combined in passes of this many fragments.
-constexpr int kReduceFragChunk = 64;
-
 template <int D>
-__global__ __launch_bounds__(256) void paged_streamk_reduce_kernel(const StreamReduceArgs a) {
-    __shared__ float s_w[4][16][kReduceFragChunk];  // per wave: weights w[g][i]
-    __shared__ float s_M[4][16];
-    __shared__ float s_den[4][16];
-    const int lane = threadIdx.x & 63;
-    const int wv = threadIdx.x >> 6;
-    const int w = blockIdx.x * 4 + wv;
-    if (w >= a.W) return;
+__global__ __launch_bounds__(kReduceThreads) void paged_streamk_reduce_kernel(const StreamReduceArgs a) {
+    const int w = blockIdx.x;
+    const int g = blockIdx.y;
     const long long* m = a.meta + 4 * w;
     if (m[0] < 0) return;
     const int TS = a.Hkv * a.nhc;
@@ -738,14 +714,14 @@ __global__ __launch_bounds__(256) void paged_streamk_reduce_kernel(const StreamR
     const int ta = ustart / q;
     if (team != ta + 1 || ustart == team * q) return;  // not the owner
     const int member = w - team * TS;
-    const int s = static_cast<int>(m[1]);
-    const int nb = static_cast<int>(m[2]);
-    const int P = (ustart + nb - 1) / q - ta + 1;
     const int kvh = member / a.nhc;
     const int hc = member - kvh * a.nhc;
     const int g0 = hc * 16;
     const int gn = min(16, a.G - g0);
-    const int h0 = kvh * a.G + g0;
+    if (g >= gn) return;
+    const int s = static_cast<int>(m[1]);
+    const int nb = static_cast<int>(m[2]);
+    const int P = (ustart + nb - 1) / q - ta + 1;
     const size_t fs = kFragHead + static_cast<size_t>(a.gstride) * D;
     // fragment i of the item comes from team ta + i
     auto frag_of = [&](int i) {
@@ -754,75 +730,11 @@ __global__ __launch_bounds__(256) void paged_streamk_reduce_kernel(const StreamR
         const int slot = (t == ta && ta * q < ustart) ? 2 * v + 1 : 2 * v;
         return a.frag + slot * fs;
     };
-    // 1. per-head max over all fragments (one parallel batch of loads per pass)
-    if (lane < gn) s_M[wv][lane] = -INFINITY;
-    __builtin_amdgcn_wave_barrier();
-    for (int c0 = 0; c0 < P; c0 += kReduceFragChunk) {
-        const int cn = min(kReduceFragChunk, P - c0);
-        for (int k = lane; k < gn * cn; k += 64) {
-            const int g = k / cn;
-            s_w[wv][g][k - g * cn] = frag_of(c0 + k - g * cn)[g];
-        }
-        __builtin_amdgcn_wave_barrier();
-        if (lane < gn) {
-            float mx = s_M[wv][lane];
-            for (int i = 0; i < cn; ++i) mx = fmaxf(mx, s_w[wv][lane][i]);
-            s_M[wv][lane] = mx;
-        }
-        __builtin_amdgcn_wave_barrier();
-    }
-    if (lane < gn) s_den[wv][lane] = 0.0f;
-    const int quads = gn * (D / 4);
-    f4 acc[16 * D / 4 / 64];  // quads owned by this lane: lane, lane + 64, ...
-#pragma unroll
-    for (int k = 0; k < 16 * D / 4 / 64; ++k) acc[k] = f4{0, 0, 0, 0};
-    // 2. weights and weighted sums, kReduceFragChunk fragments per pass
-    for (int c0 = 0; c0 < P; c0 += kReduceFragChunk) {
-        const int cn = min(kReduceFragChunk, P - c0);
-        __builtin_amdgcn_wave_barrier();
-        for (int k = lane; k < gn * cn; k += 64) {
-            const int g = k / cn;
-            const float* f = frag_of(c0 + k - g * cn);
-            const float mp = f[g];
-            s_w[wv][g][k - g * cn] =
-                (mp == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mp - s_M[wv][g]) * f[16 + g];
-        }
-        __builtin_amdgcn_wave_barrier();
-        if (lane < gn) {
-            float d = s_den[wv][lane];
-            for (int i = 0; i < cn; ++i) d += s_w[wv][lane][i];
-            s_den[wv][lane] = d;
-        }
-#pragma unroll
-        for (int k = 0; k < 16 * D / 4 / 64; ++k) {
-            const int qd = lane + 64 * k;
-            if (qd < quads) {
-                const int g = qd / (D / 4);
-                const int d4 = (qd - g * (D / 4)) * 4;
-#pragma unroll 8
-                for (int i = 0; i < cn; ++i) {
-                    acc[k] += s_w[wv][g][i] *
-                              *reinterpret_cast<const f4*>(frag_of(c0 + i) + kFragHead + static_cast<size_t>(g) * D + d4);
-                }
-            }
-        }
-    }
-    __builtin_amdgcn_wave_barrier();
-    f16* ob = a.out + (static_cast<size_t>(s) * a.H + h0) * D;
-#pragma unroll
-    for (int k = 0; k < 16 * D / 4 / 64; ++k) {
-        const int qd = lane + 64 * k;
-        if (qd < quads) {
-            const int g = qd / (D / 4);
-            const int d4 = (qd - g * (D / 4)) * 4;
-            const float den = s_den[wv][g];
-            const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-            h4 o;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) o[i] = static_cast<f16>(acc[k][i] * inv);
-            *reinterpret_cast<h4*>(ob + static_cast<size_t>(g) * D + d4) = o;
-        }
-    }
+    f16* o = a.out + (static_cast<size_t>(s) * a.H + kvh * a.G + g0 + g) * D;
+    combine_head<D>(
+        P, [&](int i) { return frag_of(i)[g]; }, [&](int i) { return frag_of(i)[16 + g]; },
+        [&](int i) { return frag_of(i) + kFragHead + static_cast<size_t>(g) * D; },
+        [&](int d, float v) { o[d] = static_cast<f16>(v); });
 }
 
 // Bit-exact materialisation of one (sequence, kv head) through the tile
@@ -1029,8 +941,8 @@ V2Need v2_need(const Shape& sh, int partition_size) {
 }
 
 template <int D>
-hipError_t launch_reduce_t(const ReduceArgs& r, int S, int Hkv, hipStream_t stream) {
-    return launch(paged_reduce_kernel<D>, dim3(Hkv * r.nhc, S), dim3(kCombineThreads), 0, stream, r);
+hipError_t launch_reduce_t(const ReduceArgs& r, int S, hipStream_t stream) {
+    return launch(paged_reduce_kernel<D>, dim3(r.H, S), dim3(kReduceThreads), 0, stream, r);
 }
 
 int validate_partition(const char* who, int partition_size) {
@@ -1118,9 +1030,9 @@ int decode_balanced(void* out, void* ws, size_t ws_bytes, const void* q, const v
     r.nhc = a.nhc;
     r.W = a.W;
     r.gstride = std::min(16, a.G);
-    const dim3 rgrid((need.W + 3) / 4);
-    err = sh.D == 128 ? launch(paged_streamk_reduce_kernel<128>, rgrid, dim3(256), 0, stream, r)
-                      : launch(paged_streamk_reduce_kernel<64>, rgrid, dim3(256), 0, stream, r);
+    const dim3 rgrid(need.W, r.gstride);
+    err = sh.D == 128 ? launch(paged_streamk_reduce_kernel<128>, rgrid, dim3(kReduceThreads), 0, stream, r)
+                      : launch(paged_streamk_reduce_kernel<64>, rgrid, dim3(kReduceThreads), 0, stream, r);
     return launched(err, who);
 }
 
@@ -1178,13 +1090,11 @@ int decode_v2(void* out, void* ws, size_t ws_bytes, const void* q, const void* k
     r.ws_sum = a.ws_sum;
     r.ws_out = a.ws_out;
     r.H = a.H;
-    r.G = a.G;
-    r.nhc = a.nhc;
     r.MB = a.MB;
     r.part_blocks = a.part_blocks;
     r.MP = a.MP;
-    err = sh.D == 128 ? launch_reduce_t<128>(r, sh.S, sh.Hkv, stream)
-                      : launch_reduce_t<64>(r, sh.S, sh.Hkv, stream);
+    err = sh.D == 128 ? launch_reduce_t<128>(r, sh.S, stream)
+                      : launch_reduce_t<64>(r, sh.S, stream);
     return launched(err, who);
 }
 
