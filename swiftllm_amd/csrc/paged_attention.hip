@@ -447,6 +447,70 @@ __device__ __forceinline__ void combine_head(int P, FM fm, FL fl, FO fo, OUT out
     }
 }
 
+// The same combine on one wave, for items with few fragments: no barriers,
+// lane l owns outputs [l * D / 64, (l + 1) * D / 64) (one coalesced row of
+// the fragment per load) and up to 16 fragment loads per lane are in flight.
+// The weights of up to 64 fragments live one per lane and are broadcast with
+// readlane; the first 64 headers are loaded once.
+template <int D>
+__device__ __forceinline__ void load_row(const float* p, float (&v)[D / 64]) {
+    if constexpr (D == 128) {
+        const float2 x = *reinterpret_cast<const float2*>(p);
+        v[0] = x.x;
+        v[1] = x.y;
+    } else {
+        v[0] = *p;
+    }
+}
+
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+template <int D, typename FM, typename FL, typename FO, typename OUT>
+__device__ __forceinline__ void combine_head_wave(int P, FM fm, FL fl, FO fo, OUT out) {
+    constexpr int DL = D / 64;
+    const int lane = threadIdx.x & 63;
+    const float m0 = lane < P ? fm(lane) : -INFINITY;
+    const float l0 = lane < P ? fl(lane) : 0.0f;
+    float M = m0;
+    for (int p = 64 + lane; p < P; p += 64) M = fmaxf(M, fm(p));
+    M = wave_max(M);
+    float acc[DL];
+#pragma unroll
+    for (int j = 0; j < DL; ++j) acc[j] = 0.0f;
+    float den = 0.0f;
+    for (int c0 = 0; c0 < P; c0 += 64) {
+        float w;
+        if (c0 == 0) {
+            w = (m0 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m0 - M) * l0;
+        } else {
+            const int p = c0 + lane;
+            const float mp = p < P ? fm(p) : -INFINITY;
+            w = (mp == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mp - M) * fl(p);
+        }
+        den += w;
+        // Batches of 16 unconditional loads: lanes past the last fragment
+        // hold weight 0 and re-read the last fragment instead of branching.
+        const int cn = min(64, P - c0);
+        for (int i0 = 0; i0 < cn; i0 += 16) {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                const int i = i0 + k;  // < 64: i0 <= 48
+                const float wi = readlane_f(w, i);
+                float v[DL];
+                load_row<D>(fo(min(c0 + i, P - 1)) + lane * DL, v);
+#pragma unroll
+                for (int j = 0; j < DL; ++j) acc[j] += wi * v[j];
+            }
+        }
+    }
+    den = wave_sum(den);
+    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+#pragma unroll
+    for (int j = 0; j < DL; ++j) out(lane * DL + j, acc[j] * inv);
+}
+
 // Split-K reduce: one workgroup per (query head, sequence); sequences with a
 // single partition were written directly by the partition kernel.
 struct ReduceArgs {
@@ -460,6 +524,28 @@ struct ReduceArgs {
     int part_blocks;
     int MP;
 };
+
+// Few partitions per sequence: one wave per (query head, sequence), four
+// heads per workgroup.
+template <int D>
+__global__ __launch_bounds__(256) void paged_reduce_wave_kernel(const ReduceArgs a) {
+    const int h = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int s = blockIdx.y;
+    if (h >= a.H) return;
+    const int L = max(a.ctx[s], 0);
+    const int nblk = min((L + kBlockTokens - 1) / kBlockTokens, a.MB);
+    const int nparts = (nblk + a.part_blocks - 1) / a.part_blocks;
+    if (nparts <= 1) return;
+    const size_t row = static_cast<size_t>(s) * a.H + h;
+    const float* pm = a.ws_max + row * a.MP;
+    const float* pl = a.ws_sum + row * a.MP;
+    const float* po = a.ws_out + row * a.MP * D;
+    f16* o = a.out + row * D;
+    combine_head_wave<D>(
+        nparts, [&](int p) { return pm[p]; }, [&](int p) { return pl[p]; },
+        [&](int p) { return po + static_cast<size_t>(p) * D; },
+        [&](int d, float v) { o[d] = static_cast<f16>(v); });
+}
 
 template <int D>
 __global__ __launch_bounds__(kReduceThreads) void paged_reduce_kernel(const ReduceArgs a) {
@@ -687,8 +773,9 @@ void paged_decode_streamk_kernel(const StreamArgs a) {
     }
 }
 
-// Combines the fragments of every split item: workgroup (w, g) reduces query
-// head g of the item whose fragments wave w owns. Wave w owns the item of its
+// Combines the fragments of every split item: one wave per (w, g) reduces
+// query head g of the item whose fragments wave w owns (four heads per
+// workgroup). Wave w owns the item of its
 // first segment when that segment is split, starts inside the sequence, and
 // w's team is the first team to start inside it (every other workgroup exits
 // at once). Fragments of the item come from the waves with the same team
@@ -702,9 +789,9 @@ struct StreamReduceArgs {
 };
 
 template <int D>
-__global__ __launch_bounds__(kReduceThreads) void paged_streamk_reduce_kernel(const StreamReduceArgs a) {
+__global__ __launch_bounds__(256) void paged_streamk_reduce_kernel(const StreamReduceArgs a) {
     const int w = blockIdx.x;
-    const int g = blockIdx.y;
+    const int g = blockIdx.y * 4 + (threadIdx.x >> 6);
     const long long* m = a.meta + 4 * w;
     if (m[0] < 0) return;
     const int TS = a.Hkv * a.nhc;
@@ -731,7 +818,7 @@ __global__ __launch_bounds__(kReduceThreads) void paged_streamk_reduce_kernel(co
         return a.frag + slot * fs;
     };
     f16* o = a.out + (static_cast<size_t>(s) * a.H + kvh * a.G + g0 + g) * D;
-    combine_head<D>(
+    combine_head_wave<D>(
         P, [&](int i) { return frag_of(i)[g]; }, [&](int i) { return frag_of(i)[16 + g]; },
         [&](int i) { return frag_of(i) + kFragHead + static_cast<size_t>(g) * D; },
         [&](int d, float v) { o[d] = static_cast<f16>(v); });
@@ -940,8 +1027,18 @@ V2Need v2_need(const Shape& sh, int partition_size) {
     return n;
 }
 
+// Up to kWaveReduceMaxParts partitions per sequence a wave combines a head;
+// more partitions get a workgroup per head.
+#ifndef SWIFTLLM_WAVE_REDUCE_MAX_PARTS
+#define SWIFTLLM_WAVE_REDUCE_MAX_PARTS 16
+#endif
+constexpr int kWaveReduceMaxParts = SWIFTLLM_WAVE_REDUCE_MAX_PARTS;
+
 template <int D>
 hipError_t launch_reduce_t(const ReduceArgs& r, int S, hipStream_t stream) {
+    if (r.MP <= kWaveReduceMaxParts) {
+        return launch(paged_reduce_wave_kernel<D>, dim3((r.H + 3) / 4, S), dim3(256), 0, stream, r);
+    }
     return launch(paged_reduce_kernel<D>, dim3(r.H, S), dim3(kReduceThreads), 0, stream, r);
 }
 
@@ -1030,9 +1127,9 @@ int decode_balanced(void* out, void* ws, size_t ws_bytes, const void* q, const v
     r.nhc = a.nhc;
     r.W = a.W;
     r.gstride = std::min(16, a.G);
-    const dim3 rgrid(need.W, r.gstride);
-    err = sh.D == 128 ? launch(paged_streamk_reduce_kernel<128>, rgrid, dim3(kReduceThreads), 0, stream, r)
-                      : launch(paged_streamk_reduce_kernel<64>, rgrid, dim3(kReduceThreads), 0, stream, r);
+    const dim3 rgrid(need.W, (r.gstride + 3) / 4);
+    err = sh.D == 128 ? launch(paged_streamk_reduce_kernel<128>, rgrid, dim3(256), 0, stream, r)
+                      : launch(paged_streamk_reduce_kernel<64>, rgrid, dim3(256), 0, stream, r);
     return launched(err, who);
 }
 
