@@ -54,7 +54,7 @@ def parse():
                     help="default: v1 for config 2, v2 for configs 3 and 4")
     ap.add_argument("--partition", type=int, default=None,
                     help="v2 partition size in tokens, 0 = balanced (stream-K) scheduling; "
-                         "default 4096 for config 3, 0 for config 4")
+                         "default 4096 for config 3, 1024 for config 4")
     ap.add_argument("--rotate", type=int, default=None,
                     help="input copies rotated between calls (default 4 for decode, 8 for MoE)")
     ap.add_argument("--seed", type=int, default=0)
@@ -63,11 +63,106 @@ def parse():
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="before warmup, one device-to-device copy of this many MiB (a kernel of known "
                          "traffic that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--summarize-trace", metavar="DIR", default=None,
+                    help="no GPU work: print a markdown table of the rocprofv3 --kernel-trace --stats "
+                         "output under DIR (k_kernel_stats.csv)")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"), default=None,
+                    help="no GPU work: print the HBM traffic JSON of --kernel from two rocprofv3 --pmc "
+                         "runs (FETCH_SIZE, then WRITE_SIZE) of a bench command with --calib-copy-mib")
+    ap.add_argument("--kernel", default=None, help="kernel name substring for --summarize-pmc")
+    ap.add_argument("--alg-bytes", type=int, default=0, help="algorithmic bytes per call (--summarize-pmc)")
+    ap.add_argument("--workload", default="", help="workload label (--summarize-pmc)")
     return ap.parse_args()
+
+
+def _find_csv(d, suffix):
+    hits = sorted(Path(d).rglob(f"*{suffix}"))
+    if not hits:
+        raise SystemExit(f"no *{suffix} under {d}")
+    return hits[0]
+
+
+def _short(name):
+    """Kernel name without the return type and namespaces."""
+    name = name.replace("void ", "").replace("swiftllm::(anonymous namespace)::", "")
+    return name
+
+
+def summarize_trace(d):
+    """Markdown table of a rocprofv3 --stats kernel summary."""
+    import csv
+
+    rows = list(csv.DictReader(open(_find_csv(d, "kernel_stats.csv"))))
+    total = sum(float(r["TotalDurationNs"]) for r in rows) or 1.0
+    print("| Kernel | Calls | Average (us) | Min (us) | Max (us) | Share |")
+    print("|---|---|---|---|---|---|")
+    for r in rows:
+        print(f"| {_short(r['Name'])} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+              f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | "
+              f"{100.0 * float(r['TotalDurationNs']) / total:.1f}% |")
+
+
+def _pmc_per_kernel(d, counter):
+    """{kernel: [value per dispatch]} of one counter (KiB per dispatch)."""
+    import csv
+    from collections import defaultdict
+
+    per = defaultdict(lambda: defaultdict(float))
+    for r in csv.DictReader(open(_find_csv(d, "counter_collection.csv"))):
+        if r["Counter_Name"] != counter:
+            continue
+        per[_short(r["Kernel_Name"])][r["Dispatch_Id"]] += float(r["Counter_Value"])
+    return {k: list(v.values()) for k, v in per.items()}
+
+
+def summarize_pmc(fetch_dir, write_dir, kernel, alg_bytes, workload):
+    """HBM traffic per launch of `kernel`: FETCH_SIZE and WRITE_SIZE (KiB per
+    dispatch), each scaled by what the counter reads for the calibration copy
+    of known size that bench.py --calib-copy-mib issued in the same run (the
+    largest __amd_rocclr_copyBuffer dispatch, which reads and writes
+    --calib-copy-mib MiB)."""
+    fetch = _pmc_per_kernel(fetch_dir, "FETCH_SIZE")
+    write = _pmc_per_kernel(write_dir, "WRITE_SIZE")
+    copy = [k for k in fetch if "copyBuffer" in k]
+    if not copy:
+        raise SystemExit("no calibration copy in the FETCH_SIZE run")
+    calib_kib = float(int(os.environ.get("CALIB_MIB", "1024")) * 1024)
+    f_scale = calib_kib / max(max(fetch[copy[0]]), 1e-9)
+    w_scale = calib_kib / max(max(write[copy[0]]), 1e-9)
+    name = [k for k in fetch if kernel in k]
+    if not name:
+        raise SystemExit(f"kernel {kernel!r} not in {sorted(fetch)}")
+    name = name[0]
+    f_kib = float(np.mean(fetch[name]))
+    w_kib = float(np.mean(write.get(name, [0.0])))
+    traffic = int(round(f_kib * 1024 * f_scale + w_kib * 1024 * w_scale))
+    others = {k: {"fetch_kib": round(float(np.mean(v)), 1),
+                  "write_kib": round(float(np.mean(write.get(k, [0.0]))), 1)}
+              for k, v in fetch.items() if k != name and "copyBuffer" not in k}
+    rec = {
+        "kernel": name,
+        "workload": workload,
+        "hbm_bytes_per_launch": traffic,
+        "fetch_kib_per_dispatch_raw": round(f_kib, 1),
+        "write_kib_per_dispatch_raw": round(w_kib, 1),
+        "fetch_scale": round(f_scale, 5),
+        "write_scale": round(w_scale, 5),
+        "calibration": f"one {int(calib_kib) // 1024} MiB device-to-device hipMemcpy in the same process "
+                       f"(bench.py --calib-copy-mib): FETCH_SIZE read {max(fetch[copy[0]]):.1f} KiB and "
+                       f"WRITE_SIZE {max(write[copy[0]]):.1f} KiB for {int(calib_kib)} KiB moved each way",
+        "dispatches_averaged": len(fetch[name]),
+        "other_kernels_same_call": others,
+        "algorithmic_bytes_per_call": alg_bytes or None,
+    }
+    print(json.dumps(rec, indent=1))
 
 
 def main():
     args = parse()
+    if args.summarize_trace:
+        return summarize_trace(args.summarize_trace)
+    if args.summarize_pmc:
+        return summarize_pmc(*args.summarize_pmc, args.kernel or "", args.alg_bytes, args.workload)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}, "
@@ -97,7 +192,10 @@ def main():
     if args.variant is None:
         args.variant = "v1" if args.config == 2 else "v2"
     if args.partition is None:
-        args.partition = 4096 if args.config == 3 else 0
+        # measured defaults: 4096-token partitions for config 3 (long uniform
+        # contexts); 1024 for config 4, where the step (cache write + decode)
+        # took 195 us against 200 us balanced and 216 us single pass
+        args.partition = 4096 if args.config == 3 else 1024
     t0 = time.time()
     w = workloads.decode_config(args.config, seed=args.seed)
     sh = w.shape
