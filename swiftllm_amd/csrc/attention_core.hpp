@@ -17,6 +17,7 @@ __device__ __forceinline__ f4 mfma16(h4 a, h4 b, f4 c) {
 }
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef __fp16 h2 __attribute__((ext_vector_type(2)));
 
 // gfx950's full-rate 16 x 16 x 32 form: lane (m, q) holds k = 8q .. 8q + 7.
 __device__ __forceinline__ f4 mfma16x32(h8 a, h8 b, f4 c) {
@@ -103,7 +104,7 @@ struct WaveState {
 //   3. online softmax in fp32 in the log2 domain; the 4 token rows of query
 //      row g live in lanes g, g^16, g^32, g^48 (two xor shuffles);
 //   4. O^T[d][g] += V[d][t] P^T[t][g] with V in its stored layout and P fed
-//      as fp16 hi + lo parts (~22 bits), P = 2^15 * exp2(s - m).
+//      as fp16 hi + lo parts (~20 bits), P = 2^15 * exp2(s - m).
 // The first nv tokens of the tile exist (the rest is zeroed so stale values
 // cannot reach a sum; nv == 0: the block contributes nothing), and query row
 // g = lane % 16 of this lane sees tokens t < lim (lim <= nv).
@@ -123,20 +124,25 @@ __device__ __forceinline__ void mask_tail(int nv, int kg, h4 (&kA)[D / 16], h4 (
     }
 }
 
-// Steps 3 + 4 for one group of 16 query rows, from the two halves s0 + s1
-// of the S^T accumulator. Lane (r, kg) holds S^T[t = 4kg + i][g = r].
+// Steps 3 + 4 for one group of 16 query rows, from the S^T accumulator sc.
+// Lane (r, kg) holds S^T[t = 4kg + i][g = r].
 // PV32 runs PV on the 16x16x32 form: k = 8q + i is token 4q + i of the hi
 // half of P for i < 4 and of the lo half otherwise, so the A operand is the
 // lane's V piece twice and the B operand its hi and lo pieces side by side.
 template <int D, bool PV32 = false>
-__device__ __forceinline__ void softmax_pv(WaveState<D>& st, f4 s0, f4 s1, int lim, int kg,
+__device__ __forceinline__ void softmax_pv(WaveState<D>& st, f4 sc, int lim, int kg,
                                            const h4 (&vA)[D / 16], float scale_log2) {
     constexpr int NJ = D / 16;
     float sv[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        sv[i] = (s0[i] + s1[i]) * scale_log2;
-        if (4 * kg + i >= lim) sv[i] = -INFINITY;
+    for (int i = 0; i < 4; ++i) sv[i] = sc[i] * scale_log2;
+    // Masks only where some row sees part of the block (tail blocks, the
+    // causal diagonal): interior blocks skip the compares.
+    if (__any(lim < kBlockTokens)) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (4 * kg + i >= lim) sv[i] = -INFINITY;
+        }
     }
     float bm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
     bm = fmaxf(bm, __shfl_xor(bm, 16));
@@ -156,12 +162,17 @@ __device__ __forceinline__ void softmax_pv(WaveState<D>& st, f4 s0, f4 s1, int l
 #pragma unroll
     for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(sv[i] - m_use + kPExp);
     st.l += (p[0] + p[1]) + (p[2] + p[3]);
-    h4 ph, pl;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        ph[i] = static_cast<f16>(p[i]);
-        pl[i] = static_cast<f16>(p[i] - static_cast<float>(ph[i]));
-    }
+    // hi = p rounded toward zero to fp16, lo = the remainder (exact in fp32)
+    // rounded toward zero again: hi + lo keeps ~20 bits of p. The packed
+    // conversions make two halves per instruction.
+    const h2 h01 = __builtin_amdgcn_cvt_pkrtz(p[0], p[1]);
+    const h2 h23 = __builtin_amdgcn_cvt_pkrtz(p[2], p[3]);
+    const h2 l01 = __builtin_amdgcn_cvt_pkrtz(p[0] - static_cast<float>(h01[0]),
+                                              p[1] - static_cast<float>(h01[1]));
+    const h2 l23 = __builtin_amdgcn_cvt_pkrtz(p[2] - static_cast<float>(h23[0]),
+                                              p[3] - static_cast<float>(h23[1]));
+    const h4 ph = __builtin_bit_cast(h4, __builtin_shufflevector(h01, h23, 0, 1, 2, 3));
+    const h4 pl = __builtin_bit_cast(h4, __builtin_shufflevector(l01, l23, 0, 1, 2, 3));
     // Step 4. Lane (r, kg) accumulates O^T[d = 16J + 4kg + i][g = r].
     if constexpr (PV32) {
         const h8 p8 = cat8(ph, pl);
@@ -195,7 +206,7 @@ __device__ __forceinline__ void attend_block(WaveState<D>& st, int nv, int lim, 
             s0 = mfma16(kT, qB.get(J), s0);
         }
     }
-    softmax_pv<D>(st, s0, s1, lim, kg, vA, scale_log2);
+    softmax_pv<D>(st, s0 + s1, lim, kg, vA, scale_log2);
 }
 
 // The same block for two groups of 16 query rows that share the kv head:
@@ -212,21 +223,18 @@ __device__ __forceinline__ void attend_block_pair(WaveState<D>& sa, WaveState<D>
                                                   h4 ident, float scale_log2) {
     constexpr int NJ = D / 16;
     mask_tail<D>(nv, kg, kA, vA);
-    f4 a0 = f4{0, 0, 0, 0}, a1 = f4{0, 0, 0, 0}, b0 = f4{0, 0, 0, 0}, b1 = f4{0, 0, 0, 0};
+    // One accumulator per group: the two groups' MFMAs interleave, so
+    // neither chain waits on its own previous result.
+    f4 sa_ = f4{0, 0, 0, 0}, sb_ = f4{0, 0, 0, 0};
 #pragma unroll
     for (int J = 0; J < NJ; J += 2) {
         const h8 kT = cat8(to_h4(mfma16(kA[J], ident, f4{0, 0, 0, 0})),
                            to_h4(mfma16(kA[J + 1], ident, f4{0, 0, 0, 0})));
-        if (J & 2) {
-            a1 = mfma16x32(kT, cat8(qa.get(J), qa.get(J + 1)), a1);
-            b1 = mfma16x32(kT, cat8(qb.get(J), qb.get(J + 1)), b1);
-        } else {
-            a0 = mfma16x32(kT, cat8(qa.get(J), qa.get(J + 1)), a0);
-            b0 = mfma16x32(kT, cat8(qb.get(J), qb.get(J + 1)), b0);
-        }
+        sa_ = mfma16x32(kT, cat8(qa.get(J), qa.get(J + 1)), sa_);
+        sb_ = mfma16x32(kT, cat8(qb.get(J), qb.get(J + 1)), sb_);
     }
-    softmax_pv<D, true>(sa, a0, a1, lim_a, kg, vA, scale_log2);
-    softmax_pv<D, true>(sb, b0, b1, lim_b, kg, vA, scale_log2);
+    softmax_pv<D, true>(sa, sa_, lim_a, kg, vA, scale_log2);
+    softmax_pv<D, true>(sb, sb_, lim_b, kg, vA, scale_log2);
 }
 
 // Every query row sees the same nv tokens (decode).
