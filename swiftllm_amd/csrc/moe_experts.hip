@@ -14,8 +14,10 @@
 //   c[rows, :] = a[rows, :] . w[e]^T, or with a second weight (gated)
 //   c = silu(a . w[e]^T) * (a . w2[e]^T). fp16 in, fp32 accumulate, fp16 out.
 //   Workgroup tile 256 activation rows x 256 weight rows (plain: 256 output
-//   columns; gated: 128 gate rows and their 128 up rows), k in steps of 64
-//   staged through double-buffered LDS (147 KiB); eight waves of 128 x 64,
+//   columns; gated: 128 gate rows and their 128 up rows), k in steps of 32
+//   copied from memory straight into a 4-stage LDS ring (global_load_lds,
+//   128 KiB, three stages in flight, rows swizzled by 16-byte chunk so the
+//   operand reads are free of bank conflicts); eight waves of 128 x 64,
 //   each on v_mfma_f32_32x32x16_f16 with the weight as the MFMA's row
 //   operand, so a lane ends with 4 consecutive output columns of one row
 //   (8-byte stores) and, gated, holds the gate and up value of each of its
@@ -39,11 +41,14 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBM = 256;        // activation rows per workgroup tile
 constexpr int kBW = 256;        // weight rows per workgroup tile (gated: 128 gate + 128 up)
-constexpr int kBK = 64;         // k per LDS stage
-constexpr int kPad = 8;         // halfs of padding per LDS row (bank spread)
-constexpr int kLdsRow = kBK + kPad;
+constexpr int kBK = 32;         // k per LDS stage
+constexpr int kKMult = 64;      // k must be a multiple of this (the API's contract)
+constexpr int kStages = 4;      // LDS stages: three in flight while one is multiplied
 constexpr int kThreads = 512;   // 8 waves: 2 (rows) x 4 (weight rows), 128 x 64 each
-constexpr int kChunks = kBM * kBK / 8 / kThreads;  // 16-byte loads per thread per tile
+constexpr int kRowChunks = kBK / 8;                        // 16-byte chunks per tile row
+constexpr int kTileChunks = kBM * kRowChunks;              // chunks per operand tile
+constexpr int kLoads = kTileChunks / kThreads;             // direct loads per thread per tile
+constexpr size_t kStageHalfs = static_cast<size_t>(kBM + kBW) * kBK;
 constexpr int kMaxE = 256;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kXcds = 8;                 // MI355X: 8 XCDs, each with its own L2
@@ -127,36 +132,56 @@ __global__ __launch_bounds__(kThreads) void moe_expert_gemm_kernel(const GemmArg
     if (row0 < 0 || row0 >= row_end) return;
     const int col0 = nt * tile_cols<GATED>();
 
-    f16* lx = lds;                       // [2][kBM][kLdsRow]
-    f16* lw = lds + 2 * kBM * kLdsRow;   // [2][kBW][kLdsRow]
+    // LDS: kStages stages, each the activation tile [kBM][kBK] and the weight
+    // tile [kBW][kBK]. A row's 16-byte chunk c lives at chunk slot
+    // c ^ ((row / 4) % 4) of the row, so the 16 rows an MFMA operand read
+    // serves at once fall in 16 different bank groups.
     const size_t K = static_cast<size_t>(a.k);
     const f16* wbase = a.w + (static_cast<size_t>(e) * a.n + col0) * K;
     const f16* w2base = GATED ? a.w2 + (static_cast<size_t>(e) * a.n + col0) * K : nullptr;
+    auto cslot = [](int r, int c) { return r * kRowChunks + (c ^ ((r >> 2) & (kRowChunks - 1))); };
 
-    // Loader: thread tid moves 16-byte chunks c = tid + 512 j of each tile
-    // (row c / 8, k chunk c % 8). Rows past the expert repeat its last row.
-    // Gated: weight rows 0..127 of the tile are gate rows, 128..255 up rows.
-    u32x4 rx[kChunks], rw[kChunks];
-    auto load_stage = [&](int k0) {
+    // Stage loader: global memory straight into LDS (global_load_lds_dwordx4).
+    // Load j of wave wv fills chunk slots (j * 8 + wv) * 64 + lane of each
+    // tile; the lane fetches the (row, chunk) that belongs there. Rows past
+    // the expert repeat its last row. Gated: weight rows 0..127 of the tile
+    // are gate rows, 128..255 up rows. Stages past the end of k reload the
+    // last one (into a buffer nobody reads again), so every iteration has the
+    // same number of loads in flight.
+    const int nk = a.k / kBK;
+    // Per-lane sources of load j (the k offset moves per stage).
+    const f16* asrc[kLoads];
+    const f16* wsrc[kLoads];
 #pragma unroll
-        for (int j = 0; j < kChunks; ++j) {
-            const int c = tid + kThreads * j;
-            const int r = c >> 3, kc = (c & 7) * 8;
-            const int row = min(row0 + r, row_end - 1);
-            rx[j] = *reinterpret_cast<const u32x4*>(a.a + static_cast<size_t>(row) * K + k0 + kc);
-            const f16* wr = (GATED && r >= kBW / 2) ? w2base + static_cast<size_t>(r - kBW / 2) * K
-                                                    : wbase + static_cast<size_t>(r) * K;
-            rw[j] = *reinterpret_cast<const u32x4*>(wr + k0 + kc);
+    for (int j = 0; j < kLoads; ++j) {
+        const int sl = (j * (kThreads / 64) + wv) * 64 + lane;
+        const int r = sl / kRowChunks;
+        const int c = (sl % kRowChunks) ^ ((r >> 2) & (kRowChunks - 1));
+        const int row = min(row0 + r, row_end - 1);
+        asrc[j] = a.a + static_cast<size_t>(row) * K + 8 * c;
+        wsrc[j] = ((GATED && r >= kBW / 2) ? w2base + static_cast<size_t>(r - kBW / 2) * K
+                                           : wbase + static_cast<size_t>(r) * K) + 8 * c;
+    }
+    auto issue_stage = [&](int ks_idx) {
+        const int k0 = min(ks_idx, nk - 1) * kBK;
+        f16* lx = lds + static_cast<size_t>(ks_idx % kStages) * kStageHalfs;
+        f16* lw = lx + kBM * kBK;
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j) {
+            const int first = (j * (kThreads / 64) + wv) * 64;  // chunk slot of lane 0
+            __builtin_amdgcn_global_load_lds(asrc[j] + k0, lx + first * 8, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(wsrc[j] + k0, lw + first * 8, 16, 0, 0);
         }
     };
-    auto store_stage = [&](int buf) {
-#pragma unroll
-        for (int j = 0; j < kChunks; ++j) {
-            const int c = tid + kThreads * j;
-            const int r = c >> 3, kc = (c & 7) * 8;
-            *reinterpret_cast<u32x4*>(lx + (buf * kBM + r) * kLdsRow + kc) = rx[j];
-            *reinterpret_cast<u32x4*>(lw + (buf * kBW + r) * kLdsRow + kc) = rw[j];
-        }
+    // Waits until this thread's loads of a stage landed while the loads of
+    // the kStages - 2 later stages stay in flight, then a bare barrier (a
+    // __syncthreads fence would wait for every load). The empty asm
+    // statements keep the compiler from moving LDS reads across it.
+    auto stage_ready = [&]() {
+        __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8) | (2 * kLoads * (kStages - 2)));
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
     };
 
     // Wave (wm, wn): activation rows wm*128 .. +128 as 4 MFMA column tiles
@@ -171,36 +196,40 @@ __global__ __launch_bounds__(kThreads) void moe_expert_gemm_kernel(const GemmArg
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f16x{};
 
-    const int nk = a.k / kBK;
-    load_stage(0);
-    store_stage(0);
-    __syncthreads();
-    const int lr = lane & 31;          // MFMA row / column within a 32 tile
-    const int lk = (lane >> 5) * 8;    // k offset of this lane's 8 values
-    for (int kt = 0; kt < nk; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) load_stage((kt + 1) * kBK);
-        const f16* bx = lx + buf * kBM * kLdsRow;
-        const f16* bw = lw + buf * kBW * kLdsRow;
 #pragma unroll
-        for (int ks = 0; ks < kBK; ks += 16) {
+    for (int st = 0; st < kStages - 1; ++st) issue_stage(st);
+    const int lr = lane & 31;          // MFMA row / column within a 32 tile
+    const int lc = lane >> 5;          // which 8 of the 16 k of an MFMA step
+    for (int kt = 0; kt < nk; ++kt) {
+        stage_ready();
+        const f16* bx = lds + static_cast<size_t>(kt % kStages) * kStageHalfs;
+        const f16* bw = bx + kBM * kBK;
+#pragma unroll
+        for (int ks = 0; ks < kBK / 16; ++ks) {
+            const int c = 2 * ks + lc;
             h8 xo[4], wo[2];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                xo[j] = *reinterpret_cast<const h8*>(bx + (wm * 128 + j * 32 + lr) * kLdsRow + ks + lk);
+                const int r = wm * 128 + j * 32 + lr;
+                xo[j] = *reinterpret_cast<const h8*>(bx + cslot(r, c) * 8);
             }
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                wo[i] = *reinterpret_cast<const h8*>(bw + (wrow(i) + lr) * kLdsRow + ks + lk);
+                const int r = wrow(i) + lr;
+                wo[i] = *reinterpret_cast<const h8*>(bw + cslot(r, c) * 8);
             }
+            // The buffer of stage kt + 3 was last read in iteration kt - 1,
+            // which every wave finished before the barrier above. Issued after
+            // the first operand reads so those start right after the barrier.
+            if (ks == 0) issue_stage(kt + kStages - 1);
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) acc[i][j] = mfma32(wo[i], xo[j], acc[i][j]);
         }
-        if (kt + 1 < nk) store_stage(buf ^ 1);
-        __syncthreads();
     }
+    // No load may still be writing this workgroup's LDS when it exits.
+    __builtin_amdgcn_s_waitcnt(0);
 
     // Epilogue: lane holds output row (tile j) lr and, per weight tile i,
     // columns q*8 + (lane/32)*4 + 0..3, q = 0..3.
@@ -284,7 +313,7 @@ int swiftllm_hip_moe_expert_gemm(const void* a, const void* w, const void* w2,
                     num_experts, m_total, n, k);
     }
     const int cols = (w2 != nullptr) ? tile_cols<true>() : tile_cols<false>();
-    if (num_experts > kMaxE || n % cols != 0 || k % kBK != 0) {
+    if (num_experts > kMaxE || n % cols != 0 || k % kKMult != 0) {
         return fail(SWIFTLLM_ERR_NOT_SUPPORTED,
                     "%s: num_experts=%d n=%d k=%d (supported: E <= 256, n a multiple of %d, k of 64)",
                     who, num_experts, n, k, cols);
@@ -318,10 +347,10 @@ int swiftllm_hip_moe_expert_gemm(const void* a, const void* w, const void* w2,
     if (grid > 0x7fffffffLL) {
         return fail(SWIFTLLM_ERR_NOT_SUPPORTED, "%s: %lld tiles", who, grid);
     }
-    // Dynamic LDS: two stages of the activation and weight tiles (147 KiB),
-    // above the default limit, so the limit is raised.
+    // Dynamic LDS: kStages stages of the activation and weight tiles
+    // (128 KiB), above the default limit, so the limit is raised.
     const bool gated = (w2 != nullptr);
-    const size_t lds = 2 * (kBM + kBW) * kLdsRow * sizeof(f16);
+    const size_t lds = kStages * kStageHalfs * sizeof(f16);
     const void* fn = gated ? reinterpret_cast<const void*>(moe_expert_gemm_kernel<true>)
                            : reinterpret_cast<const void*>(moe_expert_gemm_kernel<false>);
     hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
