@@ -317,3 +317,52 @@ def test_pool_past_two_gigaelements(dev):
         assert_attention_close(out.numpy(), ref, f"v2 ps={ps} on a 140k-block pool")
     kc.free()
     vc.free()
+
+
+def _random_batch(rng, lens, H, Hkv, D, std=1.0, extra_blocks=4):
+    """A decode workload with the given context lengths over a permuted pool."""
+    lens = np.asarray(lens, np.int32)
+    need = (np.maximum(lens, 0) + 15) // 16
+    MB = max(int(need.max()), 1)
+    NB = int(need.sum()) + extra_blocks
+    perm = rng.permutation(NB).astype(np.int32)
+    bt = np.zeros((len(lens), MB), np.int32)
+    pos = 0
+    for s, n in enumerate(need):
+        bt[s, :n] = perm[pos:pos + n]
+        pos += n
+    kc = (rng.standard_normal((NB, Hkv, D, 16)) * std).astype(np.float16)
+    vc = (rng.standard_normal((NB, Hkv, D, 16)) * std).astype(np.float16)
+    q = (rng.standard_normal((len(lens), H, D)) * std).astype(np.float16)
+    return workloads.DecodeWorkload("batch", q, kc, vc, bt, lens, 1.0 / np.sqrt(D))
+
+
+@pytest.mark.parametrize("G", [8, 1])
+def test_one_long_sequence_many_fragments(dev, G):
+    """One 32768-token sequence (plus a short one) in balanced mode: the
+    sequence spans hundreds of teams, so its reduce combines more than 64
+    fragments per item (several passes of the one-wave combine); the
+    partitioned modes combine 64 and 8 partitions (workgroup reduce)."""
+    rng = np.random.default_rng(70 + G)
+    w = _random_batch(rng, [32768, 37], H=8 * G, Hkv=8, D=128)
+    dw = DeviceWorkload(w)
+    ref = _ref(w)
+    for ps in (0, 512, 4096):
+        assert_attention_close(dw.run("v2", partition_size=ps), ref, f"long G={G} ps={ps}")
+
+
+def test_more_sequences_than_the_lds_tables(dev):
+    """4500 short sequences: the single pass drops its longest-first ranking
+    (more than 1024 sequences), the partition kernel takes one item per
+    workgroup over the full grid (more than 4096), and balanced mode falls
+    back to 512-token partitions (more than 4096)."""
+    rng = np.random.default_rng(45)
+    lens = rng.integers(0, 48, size=4500)
+    w = _random_batch(rng, lens, H=4, Hkv=2, D=64)
+    dw = DeviceWorkload(w)
+    ref = _ref(w)
+    live = lens > 0
+    for variant, ps in (("v1", None), ("v2", 32), ("v2", 0)):
+        out = dw.run(variant, partition_size=ps)
+        assert np.all(out[~live] == 0), f"{variant} ps={ps}: empty sequences must be zero"
+        assert_attention_close(out[live], ref[live], f"4500 seqs {variant} ps={ps}")
