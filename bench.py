@@ -269,6 +269,23 @@ def main():
     per = np.array([a.elapsed_ms(b) * 1e3 for a, b in evs]) if evs else np.array([ms * 1e3])
     p10, p50, p90 = (float(np.percentile(per, x)) for x in (10, 50, 90))
 
+    # Config 3 as BASELINE states it (512-token partitions, 64 per sequence),
+    # timed beside the default in the same run.
+    ms512 = None
+    if args.config == 3 and args.variant == "v2" and args.partition != 512:
+        ws512 = pa.workspace(pa.paged_attention_v2_workspace_size(
+            sh["num_seqs"], sh["num_heads"], sh["num_kv_heads"], sh["head_dim"], sh["block_size"],
+            sh["max_num_blocks_per_seq"], 512), stream)
+
+        def step512(i):
+            kc, vc = pools[i % len(pools)]
+            pa.paged_attention_v2(out, ws512, q, kc, vc, bt, ctx, w.scale, sh["num_seqs"],
+                                  sh["num_heads"], sh["num_kv_heads"], sh["head_dim"],
+                                  sh["block_size"], sh["max_num_blocks_per_seq"], 512,
+                                  num_blocks=sh["num_blocks"], stream=stream)
+
+        ms512 = timed(step512, stream, max(args.steps // 4, 1), min(args.warmup, 20), 0)[0]
+
     value = kv_bytes / (ms * 1e-3) / 1e9          # KV-read GB/s
     achieved = alg_bytes / (ms * 1e-3) / 1e9      # all algorithmic bytes / kernel time
 
@@ -334,6 +351,9 @@ def main():
         },
         "cpu_baseline": cpu,
     }
+    if ms512 is not None:
+        rec["us_per_call_partition512"] = round(ms512 * 1e3, 3)
+        rec["kv_gbs_partition512"] = round(kv_bytes / (ms512 * 1e-3) / 1e9, 2)
     print(json.dumps(rec), flush=True)
 
 
