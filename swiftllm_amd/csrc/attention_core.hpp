@@ -28,6 +28,40 @@ __device__ __forceinline__ h8 cat8(h4 lo, h4 hi) {
     return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
+// Reductions over the lane pairs l, l ^ 16 and l, l ^ 32 on gfx950's
+// permlane swaps (VALU, no trip through the LDS crossbar that __shfl_xor
+// takes). With both operands equal, permlane16_swap returns each lane's own
+// value and its l ^ 16 partner's (in row order), permlane32_swap the same for
+// l ^ 32 (checked on the GPU with an in-bounds probe); both lanes of a pair
+// combine the two values in the same order.
+__device__ __forceinline__ void swap16(float v, float& lo, float& hi) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    lo = __builtin_bit_cast(float, static_cast<unsigned>(r[0]));
+    hi = __builtin_bit_cast(float, static_cast<unsigned>(r[1]));
+}
+__device__ __forceinline__ void swap32(float v, float& lo, float& hi) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    lo = __builtin_bit_cast(float, static_cast<unsigned>(r[0]));
+    hi = __builtin_bit_cast(float, static_cast<unsigned>(r[1]));
+}
+// max / sum over lanes l, l ^ 16, l ^ 32, l ^ 48.
+__device__ __forceinline__ float max_over_kg(float v) {
+    float a, b;
+    swap16(v, a, b);
+    v = fmaxf(a, b);
+    swap32(v, a, b);
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float sum_over_kg(float v) {
+    float a, b;
+    swap16(v, a, b);
+    v = a + b;
+    swap32(v, a, b);
+    return a + b;
+}
+
 __device__ __forceinline__ h4 mask_h4(h4 v, unsigned long long m) {
     return __builtin_bit_cast(h4, __builtin_bit_cast(unsigned long long, v) & m);
 }
@@ -145,8 +179,7 @@ __device__ __forceinline__ void softmax_pv(WaveState<D>& st, f4 sc, int lim, int
         }
     }
     float bm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-    bm = fmaxf(bm, __shfl_xor(bm, 16));
-    bm = fmaxf(bm, __shfl_xor(bm, 32));
+    bm = max_over_kg(bm);
     if (__any(bm > st.m)) {
         const float m_new = fmaxf(st.m, bm);
         const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);

@@ -218,8 +218,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, int s, int kvh,
     float l_run = st.l;
     f4 (&acc)[NJ] = st.acc;
     // Per-lane partial sums cover tokens 4kg..4kg+3 of every block.
-    l_run += __shfl_xor(l_run, 16);
-    l_run += __shfl_xor(l_run, 32);
+    l_run = sum_over_kg(l_run);
 
     // Merge the waves of this workgroup.
     extern __shared__ __align__(16) float smem[];
@@ -736,8 +735,7 @@ void paged_decode_streamk_kernel(const StreamArgs a) {
         attend_blocks<D>(st, btrow, j0, 1, seg, L, a.kc, a.vc, a.Hkv, a.num_blocks, kvh, loff, kg,
                          qB, ident, a.scale_log2);
         float l_run = st.l;
-        l_run += __shfl_xor(l_run, 16);
-        l_run += __shfl_xor(l_run, 32);
+        l_run = sum_over_kg(l_run);
         const float inv = (l_run > 0.0f) ? 1.0f / l_run : 0.0f;
         if (j0 == 0 && seg == nb) {
             if (r < gn) {

@@ -169,8 +169,7 @@ void paged_prefill_kernel(const PrefillArgs a) {
 
     auto store = [&](const WaveState<D>& st, bool ok, size_t qrow) {
         float l_run = st.l;
-        l_run += __shfl_xor(l_run, 16);
-        l_run += __shfl_xor(l_run, 32);
+        l_run = sum_over_kg(l_run);
         if (!ok) return;
         const float inv = (l_run > 0.0f) ? 1.0f / l_run : 0.0f;
         f16* op = a.out + qrow * D + 4 * kg;
