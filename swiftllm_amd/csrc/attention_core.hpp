@@ -66,13 +66,14 @@ __device__ __forceinline__ h4 mask_h4(h4 v, unsigned long long m) {
     return __builtin_bit_cast(h4, __builtin_bit_cast(unsigned long long, v) & m);
 }
 
+// fp32 values that are exact fp16 numbers (the identity-MFMA transpose of a
+// K slice: one product with 1.0 plus exact zeros) back to fp16, two per
+// instruction. Any rounding mode is exact for them; the packed conversion
+// rounds toward zero.
 __device__ __forceinline__ h4 to_h4(f4 v) {
-    h4 r;
-    r[0] = static_cast<f16>(v[0]);
-    r[1] = static_cast<f16>(v[1]);
-    r[2] = static_cast<f16>(v[2]);
-    r[3] = static_cast<f16>(v[3]);
-    return r;
+    const h2 lo = __builtin_amdgcn_cvt_pkrtz(v[0], v[1]);
+    const h2 hi = __builtin_amdgcn_cvt_pkrtz(v[2], v[3]);
+    return __builtin_bit_cast(h4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3));
 }
 
 // A block id names a block of the pool: never negative, and below the pool
