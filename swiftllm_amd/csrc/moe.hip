@@ -93,10 +93,21 @@ __device__ __forceinline__ void select_topk(const float* row, int E, float (&bv)
 #pragma unroll
     for (int k = 0; k < K; ++k) bi[k] = -1;
     if (E <= kRouteRegs) {
-        // All loads issued together; the K passes then run on registers.
+        // All loads issued together (16-byte loads when the row allows); the K
+        // passes then run on registers.
         float v[kRouteRegs];
+        if ((E & 3) == 0 && (reinterpret_cast<uintptr_t>(row) & 15) == 0) {
+            typedef float f4v __attribute__((ext_vector_type(4)));
 #pragma unroll
-        for (int e = 0; e < kRouteRegs; ++e) v[e] = (e < E) ? row[e] : 0.0f;
+            for (int q = 0; q < kRouteRegs / 4; ++q) {
+                const f4v x = (4 * q < E) ? reinterpret_cast<const f4v*>(row)[q] : f4v{0, 0, 0, 0};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[4 * q + i] = x[i];
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < kRouteRegs; ++e) v[e] = (e < E) ? row[e] : 0.0f;
+        }
 #pragma unroll
         for (int k = 0; k < K; ++k) {
             float best = 0.0f;
