@@ -46,13 +46,27 @@ __device__ __forceinline__ void swap32(float v, float& lo, float& hi) {
     lo = __builtin_bit_cast(float, static_cast<unsigned>(r[0]));
     hi = __builtin_bit_cast(float, static_cast<unsigned>(r[1]));
 }
+// max(a, b) / max(a, b, c) as the bare instructions. For the values here
+// (finite scores and -inf) they equal fmaxf; fmaxf itself costs an extra
+// v_max x, x per operand that the compiler cannot prove canonical (results
+// of lane swaps and selects), to quiet signalling NaNs.
+__device__ __forceinline__ float max2(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+__device__ __forceinline__ float max3(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
 // max / sum over lanes l, l ^ 16, l ^ 32, l ^ 48.
 __device__ __forceinline__ float max_over_kg(float v) {
     float a, b;
     swap16(v, a, b);
-    v = fmaxf(a, b);
+    v = max2(a, b);
     swap32(v, a, b);
-    return fmaxf(a, b);
+    return max2(a, b);
 }
 __device__ __forceinline__ float sum_over_kg(float v) {
     float a, b;
@@ -64,6 +78,20 @@ __device__ __forceinline__ float sum_over_kg(float v) {
 
 __device__ __forceinline__ h4 mask_h4(h4 v, unsigned long long m) {
     return __builtin_bit_cast(h4, __builtin_bit_cast(unsigned long long, v) & m);
+}
+
+// p - h[0] and p - h[1] for packed fp16 h, each one v_fma_mix_f32 reading
+// the fp16 half directly (p + (-h) * 1.0, rounded once: the same value as
+// converting h to fp32 and subtracting).
+__device__ __forceinline__ float sub_h2_lo(float p, h2 h) {
+    float r;
+    asm("v_fma_mix_f32 %0, -%1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(p));
+    return r;
+}
+__device__ __forceinline__ float sub_h2_hi(float p, h2 h) {
+    float r;
+    asm("v_fma_mix_f32 %0, -%1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(p));
+    return r;
 }
 
 // fp32 values that are exact fp16 numbers (the identity-MFMA transpose of a
@@ -179,7 +207,7 @@ __device__ __forceinline__ void softmax_pv(WaveState<D>& st, f4 sc, int lim, int
             if (4 * kg + i >= lim) sv[i] = -INFINITY;
         }
     }
-    float bm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    float bm = max2(max3(sv[0], sv[1], sv[2]), sv[3]);
     bm = max_over_kg(bm);
     if (__any(bm > st.m)) {
         const float m_new = fmaxf(st.m, bm);
@@ -192,19 +220,18 @@ __device__ __forceinline__ void softmax_pv(WaveState<D>& st, f4 sc, int lim, int
     // While no valid token has been seen (an out-of-pool block, nv == 0) the
     // max is still -inf and every sv is -inf: use 0 so the weights are 0.
     const float m_use = (st.m == -INFINITY) ? 0.0f : st.m;
+    const float c = m_use - kPExp;
     float p[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(sv[i] - m_use + kPExp);
+    for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(sv[i] - c);
     st.l += (p[0] + p[1]) + (p[2] + p[3]);
     // hi = p rounded toward zero to fp16, lo = the remainder (exact in fp32)
     // rounded toward zero again: hi + lo keeps ~20 bits of p. The packed
     // conversions make two halves per instruction.
     const h2 h01 = __builtin_amdgcn_cvt_pkrtz(p[0], p[1]);
     const h2 h23 = __builtin_amdgcn_cvt_pkrtz(p[2], p[3]);
-    const h2 l01 = __builtin_amdgcn_cvt_pkrtz(p[0] - static_cast<float>(h01[0]),
-                                              p[1] - static_cast<float>(h01[1]));
-    const h2 l23 = __builtin_amdgcn_cvt_pkrtz(p[2] - static_cast<float>(h23[0]),
-                                              p[3] - static_cast<float>(h23[1]));
+    const h2 l01 = __builtin_amdgcn_cvt_pkrtz(sub_h2_lo(p[0], h01), sub_h2_hi(p[1], h01));
+    const h2 l23 = __builtin_amdgcn_cvt_pkrtz(sub_h2_lo(p[2], h23), sub_h2_hi(p[3], h23));
     const h4 ph = __builtin_bit_cast(h4, __builtin_shufflevector(h01, h23, 0, 1, 2, 3));
     const h4 pl = __builtin_bit_cast(h4, __builtin_shufflevector(l01, l23, 0, 1, 2, 3));
     // Step 4. Lane (r, kg) accumulates O^T[d = 16J + 4kg + i][g = r].
