@@ -192,13 +192,16 @@ __device__ __forceinline__ void mask_tail(int nv, int kg, h4 (&kA)[D / 16], h4 (
 // PV32 runs PV on the 16x16x32 form: k = 8q + i is token 4q + i of the hi
 // half of P for i < 4 and of the lo half otherwise, so the A operand is the
 // lane's V piece twice and the B operand its hi and lo pieces side by side.
-template <int D, bool PV32 = false>
+// FOLD (scale_log2 > 0 only): the max is taken on the unscaled scores and
+// scaled once per row (a positive factor keeps the max in place, exactly),
+// and each score's scale goes into the fused multiply-add before exp2.
+template <int D, bool PV32 = false, bool FOLD = false>
 __device__ __forceinline__ void softmax_pv(WaveState<D>& st, f4 sc, int lim, int kg,
                                            const h4 (&vA)[D / 16], float scale_log2) {
     constexpr int NJ = D / 16;
     float sv[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sv[i] = sc[i] * scale_log2;
+    for (int i = 0; i < 4; ++i) sv[i] = FOLD ? sc[i] : sc[i] * scale_log2;
     // Masks only where some row sees part of the block (tail blocks, the
     // causal diagonal): interior blocks skip the compares.
     if (__any(lim < kBlockTokens)) {
@@ -209,6 +212,7 @@ __device__ __forceinline__ void softmax_pv(WaveState<D>& st, f4 sc, int lim, int
     }
     float bm = max2(max3(sv[0], sv[1], sv[2]), sv[3]);
     bm = max_over_kg(bm);
+    if constexpr (FOLD) bm *= scale_log2;
     if (__any(bm > st.m)) {
         const float m_new = fmaxf(st.m, bm);
         const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
@@ -223,7 +227,9 @@ __device__ __forceinline__ void softmax_pv(WaveState<D>& st, f4 sc, int lim, int
     const float c = m_use - kPExp;
     float p[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(sv[i] - c);
+    for (int i = 0; i < 4; ++i) {
+        p[i] = __builtin_amdgcn_exp2f(FOLD ? __builtin_fmaf(sv[i], scale_log2, -c) : sv[i] - c);
+    }
     st.l += (p[0] + p[1]) + (p[2] + p[3]);
     // hi = p rounded toward zero to fp16, lo = the remainder (exact in fp32)
     // rounded toward zero again: hi + lo keeps ~20 bits of p. The packed
@@ -276,7 +282,7 @@ __device__ __forceinline__ void attend_block(WaveState<D>& st, int nv, int lim, 
 // with k = 8q + i read as d = 16 J0 + 4q + i for i < 4 and 16 J1 + 4q + i - 4
 // otherwise, the A operand is the lane's two transposed slices side by side
 // and the B operand its two Q pieces side by side.
-template <int D>
+template <int D, bool FOLD = false>
 __device__ __forceinline__ void attend_block_pair(WaveState<D>& sa, WaveState<D>& sb, int nv,
                                                   int lim_a, int lim_b, int kg,
                                                   h4 (&kA)[D / 16], h4 (&vA)[D / 16],
@@ -294,8 +300,8 @@ __device__ __forceinline__ void attend_block_pair(WaveState<D>& sa, WaveState<D>
         sa_ = mfma16x32(kT, cat8(qa.get(J), qa.get(J + 1)), sa_);
         sb_ = mfma16x32(kT, cat8(qb.get(J), qb.get(J + 1)), sb_);
     }
-    softmax_pv<D, true>(sa, sa_, lim_a, kg, vA, scale_log2);
-    softmax_pv<D, true>(sb, sb_, lim_b, kg, vA, scale_log2);
+    softmax_pv<D, true, FOLD>(sa, sa_, lim_a, kg, vA, scale_log2);
+    softmax_pv<D, true, FOLD>(sb, sb_, lim_b, kg, vA, scale_log2);
 }
 
 // Every query row sees the same nv tokens (decode).

@@ -55,7 +55,9 @@ struct PrefillArgs {
     int num_blocks;      // bound on block ids; <= 0: unbounded
 };
 
-template <int D>
+// FOLD: scale_log2 > 0 (the usual 1/sqrt(D)), whose scale then goes into the
+// softmax's exp2 argument.
+template <int D, bool FOLD>
 __global__ __launch_bounds__(64 * kPrefillWaves) __attribute__((amdgpu_waves_per_eu(2)))
 void paged_prefill_kernel(const PrefillArgs a) {
     constexpr int NJ = D / 16;
@@ -138,7 +140,7 @@ void paged_prefill_kernel(const PrefillArgs a) {
         const int nv = block_ok(b, a.num_blocks) ? min(kBlockTokens, L - base) : 0;
         const int lim_a = ok_a ? min(max(tqa + 1 - base, 0), nv) : 0;
         const int lim_b = ok_b ? min(max(tqb + 1 - base, 0), nv) : 0;
-        attend_block_pair<D>(sa, sb, nv, lim_a, lim_b, kg, k, v, qa, qb, ident, a.scale_log2);
+        attend_block_pair<D, FOLD>(sa, sb, nv, lim_a, lim_b, kg, k, v, qa, qb, ident, a.scale_log2);
     };
     {
         h4 kA[NJ], vA[NJ], kB[NJ], vB[NJ];
@@ -235,9 +237,13 @@ int prefill(const char* who, void* out, const void* q, const void* kc, const voi
     a.num_blocks = num_blocks;
     const dim3 grid(static_cast<unsigned>(a.groups), static_cast<unsigned>(a.Hkv * a.nhc),
                     static_cast<unsigned>(S));
-    const hipError_t err = D == 128
-        ? launch(paged_prefill_kernel<128>, grid, dim3(64 * kPrefillWaves), 0, stream, a)
-        : launch(paged_prefill_kernel<64>, grid, dim3(64 * kPrefillWaves), 0, stream, a);
+    const dim3 block(64 * kPrefillWaves);
+    const bool fold = a.scale_log2 > 0.0f;
+    const hipError_t err =
+        D == 128 ? (fold ? launch(paged_prefill_kernel<128, true>, grid, block, 0, stream, a)
+                         : launch(paged_prefill_kernel<128, false>, grid, block, 0, stream, a))
+                 : (fold ? launch(paged_prefill_kernel<64, true>, grid, block, 0, stream, a)
+                         : launch(paged_prefill_kernel<64, false>, grid, block, 0, stream, a));
     return launched(err, who);
 }
 

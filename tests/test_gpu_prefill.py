@@ -4,6 +4,8 @@ packed prompts of ragged lengths around block edges, GQA groups from 1 to
 32, head_dim 64 and 128, NaN in every unused cache slot, the bounded status
 entry, the bindings twin and PagedAttention.prefill."""
 
+import dataclasses
+
 import numpy as np
 import pytest
 
@@ -54,6 +56,16 @@ def test_prefill_long_prompts(dev, entry):
     """Llama-3-8B layer heads, two long prompts and a short one."""
     w = workloads.prefill_config((1024, 517, 3), 32, 8, 128, seed=7)
     assert_attention_close(_run(w, entry), _ref(w), f"prefill long {entry}")
+
+
+@pytest.mark.parametrize("scale", [-0.0883883, 0.0, 0.3])
+def test_prefill_scale_signs(dev, scale):
+    """A positive scale takes the kernel's path with the scale folded into the
+    exp2 argument (max on unscaled scores); zero and negative scales take the
+    plain path (max on scaled scores). Both against the oracle."""
+    w = dataclasses.replace(workloads.prefill_config((1, 17, 70, 129), 32, 8, 128, seed=11),
+                            scale=scale)
+    assert_attention_close(_run(w), _ref(w), f"prefill scale {scale}")
 
 
 def test_prefill_empty_and_zero_length_sequences(dev):
