@@ -176,7 +176,9 @@ struct WaveState {
 template <int D>
 __device__ __forceinline__ void mask_tail(int nv, int kg, h4 (&kA)[D / 16], h4 (&vA)[D / 16]) {
     constexpr int NJ = D / 16;
-    if (nv < kBlockTokens) {
+    // nv is the same in every lane: a scalar branch, which the compiler would
+    // otherwise turn into an all-ones mask ANDed into every tile register.
+    if (__builtin_amdgcn_readfirstlane(nv) < kBlockTokens) [[unlikely]] {
         const int c = min(max(nv - 4 * kg, 0), 4);
         const unsigned long long m = (c >= 4) ? ~0ull : ((1ull << (16 * c)) - 1ull);
 #pragma unroll
