@@ -11,6 +11,10 @@ namespace attn {
 constexpr float kLog2e = 1.4426950408889634f;
 // Probabilities are produced as 2^kPExp * exp2(s - m) (<= 2^15 < 65504).
 constexpr float kPExp = 15.0f;
+// Lazy rescaling: as 2^kPExpLazy * exp2(s - m) with m allowed to lag the true
+// running max by up to kLazyMargin, so they stay <= 2^(7 + 8) = 2^15.
+constexpr float kPExpLazy = 7.0f;
+constexpr float kLazyMargin = 8.0f;
 
 __device__ __forceinline__ f4 mfma16(h4 a, h4 b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
@@ -197,7 +201,12 @@ __device__ __forceinline__ void mask_tail(int nv, int kg, h4 (&kA)[D / 16], h4 (
 // FOLD (scale_log2 > 0 only): the max is taken on the unscaled scores and
 // scaled once per row (a positive factor keeps the max in place, exactly),
 // and each score's scale goes into the fused multiply-add before exp2.
-template <int D, bool PV32 = false, bool FOLD = false>
+// LAZY: the accumulators are rescaled only when some row's max grows by more
+// than kLazyMargin (log2 units); otherwise m stays behind and the weights
+// carry the difference, at most 2^kLazyMargin. Weights are 2^kPExpLazy *
+// exp2(s - m). Below 2^-3 the fp16 lo half of a weight is subnormal: its
+// error, at most 2^-24, is under 2^-31 of the row sum (>= 2^7).
+template <int D, bool PV32 = false, bool FOLD = false, bool LAZY = false>
 __device__ __forceinline__ void softmax_pv(WaveState<D>& st, f4 sc, int lim, int kg,
                                            const h4 (&vA)[D / 16], float scale_log2) {
     constexpr int NJ = D / 16;
@@ -215,7 +224,7 @@ __device__ __forceinline__ void softmax_pv(WaveState<D>& st, f4 sc, int lim, int
     float bm = max2(max3(sv[0], sv[1], sv[2]), sv[3]);
     bm = max_over_kg(bm);
     if constexpr (FOLD) bm *= scale_log2;
-    if (__any(bm > st.m)) {
+    if (__any(bm > (LAZY ? st.m + kLazyMargin : st.m))) {
         const float m_new = fmaxf(st.m, bm);
         const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
 #pragma unroll
@@ -226,7 +235,7 @@ __device__ __forceinline__ void softmax_pv(WaveState<D>& st, f4 sc, int lim, int
     // While no valid token has been seen (an out-of-pool block, nv == 0) the
     // max is still -inf and every sv is -inf: use 0 so the weights are 0.
     const float m_use = (st.m == -INFINITY) ? 0.0f : st.m;
-    const float c = m_use - kPExp;
+    const float c = m_use - (LAZY ? kPExpLazy : kPExp);
     float p[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -302,8 +311,8 @@ __device__ __forceinline__ void attend_block_pair(WaveState<D>& sa, WaveState<D>
         sa_ = mfma16x32(kT, cat8(qa.get(J), qa.get(J + 1)), sa_);
         sb_ = mfma16x32(kT, cat8(qb.get(J), qb.get(J + 1)), sb_);
     }
-    softmax_pv<D, true, FOLD>(sa, sa_, lim_a, kg, vA, scale_log2);
-    softmax_pv<D, true, FOLD>(sb, sb_, lim_b, kg, vA, scale_log2);
+    softmax_pv<D, true, FOLD, true>(sa, sa_, lim_a, kg, vA, scale_log2);
+    softmax_pv<D, true, FOLD, true>(sb, sb_, lim_b, kg, vA, scale_log2);
 }
 
 // Every query row sees the same nv tokens (decode).
