@@ -143,24 +143,30 @@ void paged_prefill_kernel(const PrefillArgs a) {
         attend_block_pair<D, FOLD>(sa, sb, nv, lim_a, lim_b, kg, k, v, qa, qb, ident, a.scale_log2);
     };
     {
+        // The next block's id (a scalar load of its first slot) is fetched
+        // one block ahead, so no load waits on it; ids past the prompt's
+        // last block are clamped to it.
         h4 kA[NJ], vA[NJ], kB[NJ], vB[NJ];
         int jA = 0;
         int bA = block_at(0);
+        int bNext = block_at(min(1, nkb - 1));  // block jA + 1
         load_tile<D, false>(a.kc, a.vc, a.Hkv, a.num_blocks, bA, kvh, loff, kA, vA);
         int left = nkb;
         for (; left > 2; left -= 2) {
             const int jB = jA + 1;
-            const int bB = block_at(jB);
+            const int bB = bNext;
             load_tile<D, false>(a.kc, a.vc, a.Hkv, a.num_blocks, bB, kvh, loff, kB, vB);
+            bNext = block_at(jB + 1);
             attend(jA, bA, kA, vA);
             jA = jB + 1;
-            bA = block_at(jA);
+            bA = bNext;
             load_tile<D, false>(a.kc, a.vc, a.Hkv, a.num_blocks, bA, kvh, loff, kA, vA);
+            bNext = block_at(min(jA + 1, nkb - 1));
             attend(jB, bB, kB, vB);
         }
         if (left == 2) {
             const int jB = jA + 1;
-            const int bB = block_at(jB);
+            const int bB = bNext;
             load_tile<D, false>(a.kc, a.vc, a.Hkv, a.num_blocks, bB, kvh, loff, kB, vB);
             attend(jA, bA, kA, vA);
             attend(jB, bB, kB, vB);
