@@ -69,6 +69,9 @@ def parse():
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"), default=None,
                     help="no GPU work: print the HBM traffic JSON of --kernel from two rocprofv3 --pmc "
                          "runs (FETCH_SIZE, then WRITE_SIZE) of a bench command with --calib-copy-mib")
+    ap.add_argument("--skip-partition512", action="store_true",
+                    help="config 3: do not also time 512-token partitions in the same run (for "
+                         "profiles whose per-kernel averages should cover the main workload only)")
     ap.add_argument("--kernel", default=None, help="kernel name substring for --summarize-pmc")
     ap.add_argument("--alg-bytes", type=int, default=0, help="algorithmic bytes per call (--summarize-pmc)")
     ap.add_argument("--workload", default="", help="workload label (--summarize-pmc)")
@@ -272,7 +275,7 @@ def main():
     # Config 3 as BASELINE states it (512-token partitions, 64 per sequence),
     # timed beside the default in the same run.
     ms512 = None
-    if args.config == 3 and args.variant == "v2" and args.partition != 512:
+    if args.config == 3 and args.variant == "v2" and args.partition != 512 and not args.skip_partition512:
         ws512 = pa.workspace(pa.paged_attention_v2_workspace_size(
             sh["num_seqs"], sh["num_heads"], sh["num_kv_heads"], sh["head_dim"], sh["block_size"],
             sh["max_num_blocks_per_seq"], 512), stream)
