@@ -346,8 +346,9 @@ int swiftllm_hip_moe_route_dispatch(const float* logits, const void* x,
  * the dispatch's x_perm) and of `c` (fp16 [m_total, n]).
  *   w2 == NULL: c[rows] = a[rows] . w[e]^T
  *   w2 != NULL: c[rows] = silu(a[rows] . w[e]^T) * (a[rows] . w2[e]^T)
- * w and w2 are fp16 [E, n, k]. fp32 accumulation. n % 128 == 0 and
- * k % 64 == 0 are supported (NotSupported otherwise); E <= 256. */
+ * w and w2 are fp16 [E, n, k]. fp32 accumulation. Supported (NotSupported
+ * otherwise): n % 128 == 0 with w2, n % 256 == 0 without; k % 64 == 0 and
+ * k <= 2^21; E <= 256. */
 int swiftllm_hip_moe_expert_gemm(const void* a, const void* w, const void* w2,
                                  const int32_t* expert_offsets,
                                  int num_experts, int m_total, int n, int k,

@@ -44,6 +44,7 @@ constexpr int kBM = 256;        // activation rows per workgroup tile
 constexpr int kBW = 256;        // weight rows per workgroup tile (gated: 128 gate + 128 up)
 constexpr int kBK = 64;         // k per LDS stage: one 128-byte line of each tile row
 constexpr int kKMult = 64;      // k must be a multiple of this (the API's contract)
+constexpr int kMaxK = 1 << 21;  // k limit of the 32-bit buffer offsets
 constexpr int kStages = 2;      // LDS stages: one in flight while one is multiplied
 constexpr int kThreads = 512;   // 8 waves: 2 (rows) x 4 (weight rows), 128 x 64 each
 constexpr int kRowChunks = kBK / 8;                        // 16-byte chunks per tile row
@@ -357,10 +358,13 @@ int swiftllm_hip_moe_expert_gemm(const void* a, const void* w, const void* w2,
                     num_experts, m_total, n, k);
     }
     const int cols = (w2 != nullptr) ? tile_cols<true>() : tile_cols<false>();
-    if (num_experts > kMaxE || n % cols != 0 || k % kKMult != 0) {
+    // The kernel addresses a workgroup's 256 rows of each operand through a
+    // buffer resource with 32-bit byte offsets: 256 * 2 * k must stay below 2^31.
+    if (num_experts > kMaxE || n % cols != 0 || k % kKMult != 0 || k > kMaxK) {
         return fail(SWIFTLLM_ERR_NOT_SUPPORTED,
-                    "%s: num_experts=%d n=%d k=%d (supported: E <= 256, n a multiple of %d, k of 64)",
-                    who, num_experts, n, k, cols);
+                    "%s: num_experts=%d n=%d k=%d (supported: E <= 256, n a multiple of %d, "
+                    "k a multiple of 64 up to %d)",
+                    who, num_experts, n, k, cols, kMaxK);
     }
     if (!w || !expert_offsets || (m_total > 0 && (!a || !c))) {
         return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: null pointer", who);

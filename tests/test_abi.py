@@ -138,6 +138,21 @@ def test_moe_validation():
     assert rc == INVALID  # workspace too small
 
 
+def test_expert_gemm_validation():
+    """Shapes the grouped expert GEMM does not take are refused before any
+    device work: n not a multiple of the tile's output columns (128 with w2,
+    256 without), k not a multiple of 64 or above 2^21, E > 256."""
+    L = _lib.lib()
+    gemm = L.swiftllm_hip_moe_expert_gemm
+    assert gemm(FAKE, FAKE, FAKE, FAKE, 8, 64, 14336 + 64, 4096, FAKE, None) == UNSUP
+    assert gemm(FAKE, FAKE, None, FAKE, 8, 64, 4096 + 128, 4096, FAKE, None) == UNSUP
+    assert gemm(FAKE, FAKE, None, FAKE, 8, 64, 4096, 4096 + 32, FAKE, None) == UNSUP
+    assert gemm(FAKE, FAKE, None, FAKE, 8, 64, 4096, (1 << 21) + 64, FAKE, None) == UNSUP
+    assert gemm(FAKE, FAKE, None, FAKE, 300, 64, 4096, 4096, FAKE, None) == UNSUP
+    assert gemm(FAKE, FAKE, None, FAKE, 8, -1, 4096, 4096, FAKE, None) == INVALID
+    assert gemm(FAKE, None, None, FAKE, 8, 64, 4096, 4096, FAKE, None) == INVALID
+
+
 @pytest.mark.skipif(_hip.device_count() > 0, reason="checks the no-device path")
 def test_device_not_found_without_gpu():
     """Valid arguments on a host without a HIP device: DeviceNotFound, the
