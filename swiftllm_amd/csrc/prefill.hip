@@ -20,9 +20,13 @@
 // of one kv head, and the second group takes the next tpw tokens. Every K/V
 // tile the wave loads serves both groups, and the K tile is transposed once
 // for both. The wave walks the key blocks up to its last token with the
-// decode kernel's per-block MFMA step; each lane's query row carries its own
-// causal limit. A wave's rows are complete when its walk ends, so it writes
-// its outputs directly: no combine, no barriers.
+// per-block MFMA step shared with decode (attention_core.hpp); each lane's
+// query row carries its own causal limit. K tiles are copied unchanged into
+// the wave's LDS by direct loads and read back already transposed
+// (ds_read_b64_tr_b16), which replaces the decode step's identity-MFMA
+// transposition and its conversions (key caches that are 8- but not
+// 16-byte aligned keep that register path). A wave's rows are complete when
+// its walk ends, so it writes its outputs directly: no combine, no barriers.
 // Four waves per workgroup take consecutive token groups; workgroups go out
 // latest tokens first (the longest walks start first). K/V tiles are loaded
 // with ordinary (cached) loads: every query group of a sequence re-reads them.
@@ -57,7 +61,71 @@ struct PrefillArgs {
 
 // FOLD: scale_log2 > 0 (the usual 1/sqrt(D)), whose scale then goes into the
 // softmax's exp2 argument.
+typedef short s4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s4 lds_s4;
+
+// The K^T operand of one 16-row slice J from a K tile copied unchanged into
+// LDS ([d][16 tokens], 2 KiB per 64 rows). With lane l reading the 8 bytes at
+// element 256 J + 4 l, ds_read_b64_tr_b16 hands lane l the elements
+// K[16 J + 4 (l / 16) + i][l % 16], i = 0..3: within each 16-lane group, lane
+// i receives element i % 4 of lanes i / 4, + 4, + 8, + 12 (checked on the
+// GPU with an in-bounds probe). That is the transposed slice in the MFMA's
+// A-operand layout, the same values the identity-MFMA transposition makes.
+__device__ __forceinline__ h4 read_kT(const f16* tile, int J, int lane) {
+    const s4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_s4*)(const_cast<f16*>(tile) + 256 * J + 4 * lane));
+    return __builtin_bit_cast(h4, v);
+}
+
+// Zeroes the V columns of the tokens past nv (stale slots of a partial
+// block); nv is the same in every lane, so this is a scalar branch.
+template <int D>
+__device__ __forceinline__ void mask_v(int nv, int kg, h4 (&vA)[D / 16]) {
+    if (__builtin_amdgcn_readfirstlane(nv) < kBlockTokens) [[unlikely]] {
+        const int c = min(max(nv - 4 * kg, 0), 4);
+        const unsigned long long m = (c >= 4) ? ~0ull : ((1ull << (16 * c)) - 1ull);
+#pragma unroll
+        for (int J = 0; J < D / 16; ++J) vA[J] = mask_h4(vA[J], m);
+    }
+}
+
+// Steps 1 - 4 of one key block for both row groups, K^T read from the
+// block's K tile in LDS. Stale K columns (tokens >= nv) only reach the score
+// rows of those tokens, which the masks (lim <= nv) then replace by -inf.
 template <int D, bool FOLD>
+__device__ __forceinline__ void attend_block_pair_lds(WaveState<D>& sa, WaveState<D>& sb, int nv,
+                                                      int lim_a, int lim_b, int kg, int lane,
+                                                      const f16* ktile, h4 (&vA)[D / 16],
+                                                      const QOperand<D>& qa,
+                                                      const QOperand<D>& qb, float scale_log2) {
+    constexpr int NJ = D / 16;
+    mask_v<D>(nv, kg, vA);
+    f4 sa_ = f4{0, 0, 0, 0}, sb_ = f4{0, 0, 0, 0};
+#pragma unroll
+    for (int J = 0; J < NJ; J += 2) {
+        const h8 kT = cat8(read_kT(ktile, J, lane), read_kT(ktile, J + 1, lane));
+        sa_ = mfma16x32(kT, cat8(qa.get(J), qa.get(J + 1)), sa_);
+        sb_ = mfma16x32(kT, cat8(qb.get(J), qb.get(J + 1)), sb_);
+    }
+    softmax_pv<D, true, FOLD, true>(sa, sa_, lim_a, kg, vA, scale_log2);
+    softmax_pv<D, true, FOLD, true>(sb, sb_, lim_b, kg, vA, scale_log2);
+}
+
+// Waits until at most N of this wave's memory loads are in flight. The
+// empty asm statements keep the compiler from moving LDS reads above it.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt field");
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+    asm volatile("" ::: "memory");
+}
+
+// LDSK: K tiles go straight from memory into LDS (global_load_lds, 16 bytes
+// a lane; the key cache is 16-byte aligned) and come back transposed by
+// ds_read_b64_tr_b16; otherwise through registers and an identity-MFMA
+// transposition.
+template <int D, bool FOLD, bool LDSK>
 __global__ __launch_bounds__(64 * kPrefillWaves) __attribute__((amdgpu_waves_per_eu(2)))
 void paged_prefill_kernel(const PrefillArgs a) {
     constexpr int NJ = D / 16;
@@ -142,7 +210,83 @@ void paged_prefill_kernel(const PrefillArgs a) {
         const int lim_b = ok_b ? min(max(tqb + 1 - base, 0), nv) : 0;
         attend_block_pair<D, FOLD>(sa, sb, nv, lim_a, lim_b, kg, k, v, qa, qb, ident, a.scale_log2);
     };
-    {
+    if constexpr (LDSK) {
+        // Two K tiles per wave in LDS, double-buffered like the registers.
+        constexpr int kTileHalfs = D * kBlockTokens;
+        constexpr int kDma = kTileHalfs * 2 / (64 * 16);  // 16-byte loads per lane per tile
+        // Two arrays, so the compiler can tell a tile's reads from the other
+        // tile's loads in flight (one array made it wait for those too).
+        __shared__ __align__(16) f16 s_k0[kPrefillWaves * kTileHalfs];
+        __shared__ __align__(16) f16 s_k1[kPrefillWaves * kTileHalfs];
+        f16* const kt0 = s_k0 + w * kTileHalfs;
+        f16* const kt1 = s_k1 + w * kTileHalfs;
+        auto issue_k = [&](int b, f16* dst) {
+            // The tile's previous reads are done (its LDS is rewritten).
+            __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (0x3 << 14));  // lgkmcnt(0)
+            const int bsafe = block_ok(b, a.num_blocks) ? b : 0;
+            const f16* src = a.kc + kv_tile_offset(bsafe, kvh, a.Hkv, D) + 8 * lane;
+#pragma unroll
+            for (int j = 0; j < kDma; ++j) {
+                __builtin_amdgcn_global_load_lds(src + 512 * j, dst + 512 * j, 16, 0, 0);
+            }
+        };
+        auto load_v = [&](int b, h4 (&v)[NJ]) {
+            const int bsafe = block_ok(b, a.num_blocks) ? b : 0;
+            const f16* vp = a.vc + kv_tile_offset(bsafe, kvh, a.Hkv, D) + loff;
+#pragma unroll
+            for (int J = 0; J < NJ; ++J) v[J] = load_kv<false>(vp + kv_elem_offset(16 * J, 0));
+        };
+        auto attend_l = [&](int jb, int b, const f16* kt, h4 (&v)[NJ]) {
+            const int base = jb * kBlockTokens;
+            const int nv = block_ok(b, a.num_blocks) ? min(kBlockTokens, L - base) : 0;
+            const int lim_a = ok_a ? min(max(tqa + 1 - base, 0), nv) : 0;
+            const int lim_b = ok_b ? min(max(tqb + 1 - base, 0), nv) : 0;
+            attend_block_pair_lds<D, FOLD>(sa, sb, nv, lim_a, lim_b, kg, lane, kt, v, qa, qb,
+                                           a.scale_log2);
+        };
+        // Loads in flight behind a block's K tile: its V tile, then the next
+        // block's K tile and V tile (when there is a next block).
+        constexpr int kBehindNext = NJ + kDma + NJ;
+        constexpr int kBehindLast = NJ;
+        h4 vA[NJ], vB[NJ];
+        int jA = 0;
+        int bA = block_at(0);
+        int bNext = block_at(min(1, nkb - 1));  // block jA + 1
+        issue_k(bA, kt0);
+        load_v(bA, vA);
+        int left = nkb;
+        for (; left > 2; left -= 2) {
+            const int jB = jA + 1;
+            const int bB = bNext;
+            issue_k(bB, kt1);
+            load_v(bB, vB);
+            bNext = block_at(jB + 1);
+            wait_vm<kBehindNext>();
+            attend_l(jA, bA, kt0, vA);
+            jA = jB + 1;
+            bA = bNext;
+            issue_k(bA, kt0);
+            load_v(bA, vA);
+            bNext = block_at(min(jA + 1, nkb - 1));
+            wait_vm<kBehindNext>();
+            attend_l(jB, bB, kt1, vB);
+        }
+        if (left == 2) {
+            const int jB = jA + 1;
+            const int bB = bNext;
+            issue_k(bB, kt1);
+            load_v(bB, vB);
+            wait_vm<kBehindNext>();
+            attend_l(jA, bA, kt0, vA);
+            wait_vm<kBehindLast>();
+            attend_l(jB, bB, kt1, vB);
+        } else {
+            wait_vm<kBehindLast>();
+            attend_l(jA, bA, kt0, vA);
+        }
+        // No load may still be writing this wave's LDS when it exits.
+        __builtin_amdgcn_s_waitcnt(0);
+    } else {
         // The next block's id (a scalar load of its first slot) is fetched
         // one block ahead, so no load waits on it; ids past the prompt's
         // last block are clamped to it.
@@ -245,11 +389,15 @@ int prefill(const char* who, void* out, const void* q, const void* kc, const voi
                     static_cast<unsigned>(S));
     const dim3 block(64 * kPrefillWaves);
     const bool fold = a.scale_log2 > 0.0f;
+    const bool ldsk = aligned(kc, 16);
+    using K = void (*)(PrefillArgs);
+    static const K kernels[2][2][2] = {
+        {{paged_prefill_kernel<64, false, false>, paged_prefill_kernel<64, false, true>},
+         {paged_prefill_kernel<64, true, false>, paged_prefill_kernel<64, true, true>}},
+        {{paged_prefill_kernel<128, false, false>, paged_prefill_kernel<128, false, true>},
+         {paged_prefill_kernel<128, true, false>, paged_prefill_kernel<128, true, true>}}};
     const hipError_t err =
-        D == 128 ? (fold ? launch(paged_prefill_kernel<128, true>, grid, block, 0, stream, a)
-                         : launch(paged_prefill_kernel<128, false>, grid, block, 0, stream, a))
-                 : (fold ? launch(paged_prefill_kernel<64, true>, grid, block, 0, stream, a)
-                         : launch(paged_prefill_kernel<64, false>, grid, block, 0, stream, a));
+        launch(kernels[D == 128][fold][ldsk], grid, block, 0, stream, a);
     return launched(err, who);
 }
 

@@ -68,6 +68,27 @@ def test_prefill_scale_signs(dev, scale):
     assert_attention_close(_run(w), _ref(w), f"prefill scale {scale}")
 
 
+def test_prefill_key_cache_8_byte_aligned(dev):
+    """A key cache that is 8- but not 16-byte aligned takes the kernel's
+    register path for K (the default path copies K tiles into LDS with
+    16-byte loads); both against the oracle."""
+    w = workloads.prefill_config((1, 17, 70, 129), 32, 8, 128, seed=13)
+    T, H, D = w.q.shape
+    S = len(w.context_lens)
+    kc_buf = DeviceArray((w.key_cache.nbytes + 16,), np.uint8)
+    kc_bytes = np.zeros(w.key_cache.nbytes + 16, np.uint8)
+    kc_bytes[8:8 + w.key_cache.nbytes] = w.key_cache.view(np.uint8).ravel()
+    kc_buf.upload(kc_bytes)
+    out = DeviceArray((T, H, D), np.float16)
+    q = DeviceArray.from_numpy(w.q)
+    vc = DeviceArray.from_numpy(w.value_cache)
+    sm, ctx = DeviceArray.from_numpy(w.slot_mapping), DeviceArray.from_numpy(w.context_lens)
+    pa.launch_paged_prefill(out, q, kc_buf.ptr + 8, vc, sm, ctx, w.scale, S, H, 8, D, 16,
+                            int(w.context_lens.max()), num_blocks=w.key_cache.shape[0])
+    synchronize()
+    assert_attention_close(out.numpy(), _ref(w), "prefill, key cache at +8 bytes")
+
+
 def test_prefill_empty_and_zero_length_sequences(dev):
     w = workloads.prefill_config((0, 33, 0, 5), 8, 2, 64, seed=8)
     out = _run(w)
