@@ -272,6 +272,19 @@ def main():
     per = np.array([a.elapsed_ms(b) * 1e3 for a, b in evs]) if evs else np.array([ms * 1e3])
     p10, p50, p90 = (float(np.percentile(per, x)) for x in (10, 50, 90))
 
+    # Single-launch latency: one call on an idle GPU (the stream drained before
+    # and after), from its first event to its last.
+    single = []
+    for i in range(args.samples and 20):
+        a, b = Event(), Event()
+        stream.synchronize()
+        a.record(stream)
+        step(i)
+        b.record(stream)
+        b.synchronize()
+        single.append(a.elapsed_ms(b) * 1e3)
+    single_p50 = float(np.median(single)) if single else None
+
     # Config 3 as BASELINE states it (512-token partitions, 64 per sequence),
     # timed beside the default in the same run.
     ms512 = None
@@ -327,6 +340,7 @@ def main():
         "ms_per_step": round(ms, 6),
         "us_per_call": round(ms * 1e3, 3),
         "us_per_call_p10_p50_p90": [round(p10, 2), round(p50, 2), round(p90, 2)],
+        "us_single_launch_p50": round(single_p50, 2) if single_p50 is not None else None,
         "hbm_peak_frac": round(value / HBM_PEAK_GBS, 4),
         "higher_is_better": True,
         "scaling": "weak",
