@@ -31,6 +31,7 @@
 // latest tokens first (the longest walks start first). K/V tiles are loaded
 // with ordinary (cached) loads: every query group of a sequence re-reads them.
 
+#include <type_traits>
 #include "attention_core.hpp"
 
 namespace swiftllm {
@@ -89,28 +90,6 @@ __device__ __forceinline__ void mask_v(int nv, int kg, h4 (&vA)[D / 16]) {
     }
 }
 
-// Steps 1 - 4 of one key block for both row groups, K^T read from the
-// block's K tile in LDS. Stale K columns (tokens >= nv) only reach the score
-// rows of those tokens, which the masks (lim <= nv) then replace by -inf.
-template <int D, bool FOLD>
-__device__ __forceinline__ void attend_block_pair_lds(WaveState<D>& sa, WaveState<D>& sb, int nv,
-                                                      int lim_a, int lim_b, int kg, int lane,
-                                                      const f16* ktile, h4 (&vA)[D / 16],
-                                                      const QOperand<D>& qa,
-                                                      const QOperand<D>& qb, float scale_log2) {
-    constexpr int NJ = D / 16;
-    mask_v<D>(nv, kg, vA);
-    f4 sa_ = f4{0, 0, 0, 0}, sb_ = f4{0, 0, 0, 0};
-#pragma unroll
-    for (int J = 0; J < NJ; J += 2) {
-        const h8 kT = cat8(read_kT(ktile, J, lane), read_kT(ktile, J + 1, lane));
-        sa_ = mfma16x32(kT, cat8(qa.get(J), qa.get(J + 1)), sa_);
-        sb_ = mfma16x32(kT, cat8(qb.get(J), qb.get(J + 1)), sb_);
-    }
-    softmax_pv<D, true, FOLD, true>(sa, sa_, lim_a, kg, vA, scale_log2);
-    softmax_pv<D, true, FOLD, true>(sb, sb_, lim_b, kg, vA, scale_log2);
-}
-
 // Waits until at most N of this wave's memory loads are in flight. The
 // empty asm statements keep the compiler from moving LDS reads above it.
 template <int N>
@@ -119,6 +98,32 @@ __device__ __forceinline__ void wait_vm() {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
     asm volatile("" ::: "memory");
+}
+
+// Steps 1 - 4 of one key block for both row groups, K^T read from the
+// block's K tile in LDS. Stale K columns (tokens >= nv) only reach the score
+// rows of those tokens, which the masks (lim <= nv) then replace by -inf.
+// VWAIT: loads issued after this block's V loads; the wait for V before PV
+// is explicit, since the compiler's count of loads into LDS mixed with loads
+// into registers cannot be relied on to cover them.
+template <int D, bool FOLD, int VWAIT>
+__device__ __forceinline__ void attend_block_pair_lds(WaveState<D>& sa, WaveState<D>& sb, int nv,
+                                                      int lim_a, int lim_b, int kg, int lane,
+                                                      const f16* ktile, h4 (&vA)[D / 16],
+                                                      const QOperand<D>& qa,
+                                                      const QOperand<D>& qb, float scale_log2) {
+    constexpr int NJ = D / 16;
+    f4 sa_ = f4{0, 0, 0, 0}, sb_ = f4{0, 0, 0, 0};
+#pragma unroll
+    for (int J = 0; J < NJ; J += 2) {
+        const h8 kT = cat8(read_kT(ktile, J, lane), read_kT(ktile, J + 1, lane));
+        sa_ = mfma16x32(kT, cat8(qa.get(J), qa.get(J + 1)), sa_);
+        sb_ = mfma16x32(kT, cat8(qb.get(J), qb.get(J + 1)), sb_);
+    }
+    wait_vm<VWAIT>();
+    mask_v<D>(nv, kg, vA);
+    softmax_pv<D, true, FOLD, true>(sa, sa_, lim_a, kg, vA, scale_log2);
+    softmax_pv<D, true, FOLD, true>(sb, sb_, lim_b, kg, vA, scale_log2);
 }
 
 // LDSK: K tiles go straight from memory into LDS (global_load_lds, 16 bytes
@@ -236,18 +241,23 @@ void paged_prefill_kernel(const PrefillArgs a) {
 #pragma unroll
             for (int J = 0; J < NJ; ++J) v[J] = load_kv<false>(vp + kv_elem_offset(16 * J, 0));
         };
-        auto attend_l = [&](int jb, int b, const f16* kt, h4 (&v)[NJ]) {
+        // vw: loads issued after v's (std::integral_constant), the V wait.
+        auto attend_l = [&](auto vw, int jb, int b, const f16* kt, h4 (&v)[NJ]) {
             const int base = jb * kBlockTokens;
             const int nv = block_ok(b, a.num_blocks) ? min(kBlockTokens, L - base) : 0;
             const int lim_a = ok_a ? min(max(tqa + 1 - base, 0), nv) : 0;
             const int lim_b = ok_b ? min(max(tqb + 1 - base, 0), nv) : 0;
-            attend_block_pair_lds<D, FOLD>(sa, sb, nv, lim_a, lim_b, kg, lane, kt, v, qa, qb,
-                                           a.scale_log2);
+            attend_block_pair_lds<D, FOLD, decltype(vw)::value>(sa, sb, nv, lim_a, lim_b, kg,
+                                                                lane, kt, v, qa, qb,
+                                                                a.scale_log2);
         };
         // Loads in flight behind a block's K tile: its V tile, then the next
-        // block's K tile and V tile (when there is a next block).
+        // block's K tile and V tile (when there is a next block); behind its
+        // V tile, the next block's two tiles or nothing.
         constexpr int kBehindNext = NJ + kDma + NJ;
         constexpr int kBehindLast = NJ;
+        const std::integral_constant<int, kDma + NJ> v_next;
+        const std::integral_constant<int, 0> v_last;
         h4 vA[NJ], vB[NJ];
         int jA = 0;
         int bA = block_at(0);
@@ -262,14 +272,14 @@ void paged_prefill_kernel(const PrefillArgs a) {
             load_v(bB, vB);
             bNext = block_at(jB + 1);
             wait_vm<kBehindNext>();
-            attend_l(jA, bA, kt0, vA);
+            attend_l(v_next, jA, bA, kt0, vA);
             jA = jB + 1;
             bA = bNext;
             issue_k(bA, kt0);
             load_v(bA, vA);
             bNext = block_at(min(jA + 1, nkb - 1));
             wait_vm<kBehindNext>();
-            attend_l(jB, bB, kt1, vB);
+            attend_l(v_next, jB, bB, kt1, vB);
         }
         if (left == 2) {
             const int jB = jA + 1;
@@ -277,12 +287,12 @@ void paged_prefill_kernel(const PrefillArgs a) {
             issue_k(bB, kt1);
             load_v(bB, vB);
             wait_vm<kBehindNext>();
-            attend_l(jA, bA, kt0, vA);
+            attend_l(v_next, jA, bA, kt0, vA);
             wait_vm<kBehindLast>();
-            attend_l(jB, bB, kt1, vB);
+            attend_l(v_last, jB, bB, kt1, vB);
         } else {
             wait_vm<kBehindLast>();
-            attend_l(jA, bA, kt0, vA);
+            attend_l(v_last, jA, bA, kt0, vA);
         }
         // No load may still be writing this wave's LDS when it exits.
         __builtin_amdgcn_s_waitcnt(0);
