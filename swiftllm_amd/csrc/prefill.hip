@@ -19,13 +19,14 @@
 // is tpw = 16 / gw consecutive query tokens times gw = min(G, 16) query heads
 // of one kv head, and the second group takes the next tpw tokens. Every K/V
 // tile the wave loads serves both groups, and the K tile is transposed once
-// for both. The wave walks the key blocks up to its last token with the
-// per-block MFMA step shared with decode (attention_core.hpp); each lane's
+// for both. The wave walks the key blocks up to its last token; each lane's
 // query row carries its own causal limit. K tiles are copied unchanged into
 // the wave's LDS by direct loads and read back already transposed
-// (ds_read_b64_tr_b16), which replaces the decode step's identity-MFMA
-// transposition and its conversions (key caches that are 8- but not
-// 16-byte aligned keep that register path). A wave's rows are complete when
+// (ds_read_b64_tr_b16), and the walk goes by pairs of blocks: one softmax
+// step per 32 keys, whose PV products take the two blocks' V side by side.
+// Key caches that are 8- but not 16-byte aligned take the per-block MFMA
+// step shared with decode (attention_core.hpp: an identity-MFMA
+// transposition of K in registers). A wave's rows are complete when
 // its walk ends, so it writes its outputs directly: no combine, no barriers.
 // Four waves per workgroup take consecutive token groups; workgroups go out
 // latest tokens first (the longest walks start first). K/V tiles are loaded
@@ -78,15 +79,22 @@ __device__ __forceinline__ h4 read_kT(const f16* tile, int J, int lane) {
     return __builtin_bit_cast(h4, v);
 }
 
-// Zeroes the V columns of the tokens past nv (stale slots of a partial
-// block); nv is the same in every lane, so this is a scalar branch.
+// Zeroes the V columns of the tokens past nv0 in the low halves (the pair's
+// first block) and past nv1 in the high halves (its second block); nv0 and
+// nv1 are the same in every lane, so this is a scalar branch.
 template <int D>
-__device__ __forceinline__ void mask_v(int nv, int kg, h4 (&vA)[D / 16]) {
-    if (__builtin_amdgcn_readfirstlane(nv) < kBlockTokens) [[unlikely]] {
-        const int c = min(max(nv - 4 * kg, 0), 4);
-        const unsigned long long m = (c >= 4) ? ~0ull : ((1ull << (16 * c)) - 1ull);
+__device__ __forceinline__ void mask_v_pair(int nv0, int nv1, int kg, h8 (&vp)[D / 16]) {
+    if (__builtin_amdgcn_readfirstlane(min(nv0, nv1)) < kBlockTokens) [[unlikely]] {
+        const int c0 = min(max(nv0 - 4 * kg, 0), 4);
+        const int c1 = min(max(nv1 - 4 * kg, 0), 4);
+        const unsigned long long m0 = (c0 >= 4) ? ~0ull : ((1ull << (16 * c0)) - 1ull);
+        const unsigned long long m1 = (c1 >= 4) ? ~0ull : ((1ull << (16 * c1)) - 1ull);
 #pragma unroll
-        for (int J = 0; J < D / 16; ++J) vA[J] = mask_h4(vA[J], m);
+        for (int J = 0; J < D / 16; ++J) {
+            const h4 lo = __builtin_shufflevector(vp[J], vp[J], 0, 1, 2, 3);
+            const h4 hi = __builtin_shufflevector(vp[J], vp[J], 4, 5, 6, 7);
+            vp[J] = cat8(mask_h4(lo, m0), mask_h4(hi, m1));
+        }
     }
 }
 
@@ -100,30 +108,98 @@ __device__ __forceinline__ void wait_vm() {
     asm volatile("" ::: "memory");
 }
 
-// Steps 1 - 4 of one key block for both row groups, K^T read from the
-// block's K tile in LDS. Stale K columns (tokens >= nv) only reach the score
-// rows of those tokens, which the masks (lim <= nv) then replace by -inf.
-// VWAIT: loads issued after this block's V loads; the wait for V before PV
-// is explicit, since the compiler's count of loads into LDS mixed with loads
-// into registers cannot be relied on to cover them.
-template <int D, bool FOLD, int VWAIT>
-__device__ __forceinline__ void attend_block_pair_lds(WaveState<D>& sa, WaveState<D>& sb, int nv,
-                                                      int lim_a, int lim_b, int kg, int lane,
-                                                      const f16* ktile, h4 (&vA)[D / 16],
-                                                      const QOperand<D>& qa,
-                                                      const QOperand<D>& qb, float scale_log2) {
+// Steps 3 + 4 for one group of 16 query rows over a pair of key blocks (32
+// keys), from the S^T accumulators s0 (first block) and s1 (second): lane
+// (r, kg) holds S^T[t = 4kg + i][g = r] of each. The same online softmax as
+// the per-block step (lazy rescaling, weights 2^kPExpLazy * exp2(s - m) as
+// fp16 hi + lo parts, FOLD as there), with one row max per 32 keys. PV runs
+// on the 16x16x32 form with k = 8q + i the token 4q + i of the first block
+// for i < 4 and of the second otherwise: the A operand is the lane's V
+// pieces of the two blocks side by side (vp), the B operand the two blocks'
+// hi parts, then their lo parts.
+template <int D, bool FOLD>
+__device__ __forceinline__ void softmax_pv_pair(WaveState<D>& st, f4 s0, f4 s1, bool masked,
+                                                int lim0, int lim1, int kg,
+                                                const h8 (&vp)[D / 16], float scale_log2) {
     constexpr int NJ = D / 16;
-    f4 sa_ = f4{0, 0, 0, 0}, sb_ = f4{0, 0, 0, 0};
+    float sv[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        sv[i] = FOLD ? s0[i] : s0[i] * scale_log2;
+        sv[4 + i] = FOLD ? s1[i] : s1[i] * scale_log2;
+    }
+    if (masked) [[unlikely]] {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (4 * kg + i >= lim0) sv[i] = -INFINITY;
+            if (4 * kg + i >= lim1) sv[4 + i] = -INFINITY;
+        }
+    }
+    float bm = max3(max3(sv[0], sv[1], sv[2]), max3(sv[3], sv[4], sv[5]), max2(sv[6], sv[7]));
+    bm = max_over_kg(bm);
+    if constexpr (FOLD) bm *= scale_log2;
+    if (__any(bm > st.m + kLazyMargin)) {
+        const float m_new = fmaxf(st.m, bm);
+        const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
+#pragma unroll
+        for (int J = 0; J < NJ; ++J) st.acc[J] *= alpha;
+        st.l *= alpha;
+        st.m = m_new;
+    }
+    // No valid token seen yet: m is -inf and so is every sv; 0 keeps the
+    // weights 0.
+    const float m_use = (st.m == -INFINITY) ? 0.0f : st.m;
+    const float c = m_use - kPExpLazy;
+    float p[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        p[i] = __builtin_amdgcn_exp2f(FOLD ? __builtin_fmaf(sv[i], scale_log2, -c) : sv[i] - c);
+    }
+    st.l += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+    h2 hh[4], ll[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        hh[i] = __builtin_amdgcn_cvt_pkrtz(p[2 * i], p[2 * i + 1]);
+        ll[i] = __builtin_amdgcn_cvt_pkrtz(sub_h2_lo(p[2 * i], hh[i]),
+                                           sub_h2_hi(p[2 * i + 1], hh[i]));
+    }
+    const h8 ph = __builtin_bit_cast(
+        h8, __builtin_shufflevector(__builtin_shufflevector(hh[0], hh[1], 0, 1, 2, 3),
+                                    __builtin_shufflevector(hh[2], hh[3], 0, 1, 2, 3), 0, 1, 2,
+                                    3, 4, 5, 6, 7));
+    const h8 pl = __builtin_bit_cast(
+        h8, __builtin_shufflevector(__builtin_shufflevector(ll[0], ll[1], 0, 1, 2, 3),
+                                    __builtin_shufflevector(ll[2], ll[3], 0, 1, 2, 3), 0, 1, 2,
+                                    3, 4, 5, 6, 7));
+#pragma unroll
+    for (int J = 0; J < NJ; ++J) st.acc[J] = mfma16x32(vp[J], ph, st.acc[J]);
+#pragma unroll
+    for (int J = 0; J < NJ; ++J) st.acc[J] = mfma16x32(vp[J], pl, st.acc[J]);
+}
+
+// Steps 1 + 2 of a pair of key blocks for both row groups: S^T of the first
+// block (s[0] group a, s[1] group b) and of the second (s[2], s[3]), K^T read
+// from the pair's two K tiles in LDS (ktiles, the second D * 16 halves after
+// the first). Four independent accumulator chains.
+template <int D>
+__device__ __forceinline__ void qk_pair_lds(f4 (&s)[4], int lane, const f16* ktiles,
+                                            const QOperand<D>& qa, const QOperand<D>& qb) {
+    constexpr int NJ = D / 16;
+    constexpr int kTileHalfs = D * kBlockTokens;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[i] = f4{0, 0, 0, 0};
 #pragma unroll
     for (int J = 0; J < NJ; J += 2) {
-        const h8 kT = cat8(read_kT(ktile, J, lane), read_kT(ktile, J + 1, lane));
-        sa_ = mfma16x32(kT, cat8(qa.get(J), qa.get(J + 1)), sa_);
-        sb_ = mfma16x32(kT, cat8(qb.get(J), qb.get(J + 1)), sb_);
+        const h8 k0 = cat8(read_kT(ktiles, J, lane), read_kT(ktiles, J + 1, lane));
+        const h8 k1 = cat8(read_kT(ktiles + kTileHalfs, J, lane),
+                           read_kT(ktiles + kTileHalfs, J + 1, lane));
+        const h8 qA = cat8(qa.get(J), qa.get(J + 1));
+        const h8 qB = cat8(qb.get(J), qb.get(J + 1));
+        s[0] = mfma16x32(k0, qA, s[0]);
+        s[1] = mfma16x32(k0, qB, s[1]);
+        s[2] = mfma16x32(k1, qA, s[2]);
+        s[3] = mfma16x32(k1, qB, s[3]);
     }
-    wait_vm<VWAIT>();
-    mask_v<D>(nv, kg, vA);
-    softmax_pv<D, true, FOLD, true>(sa, sa_, lim_a, kg, vA, scale_log2);
-    softmax_pv<D, true, FOLD, true>(sb, sb_, lim_b, kg, vA, scale_log2);
 }
 
 // LDSK: K tiles go straight from memory into LDS (global_load_lds, 16 bytes
@@ -216,83 +292,145 @@ void paged_prefill_kernel(const PrefillArgs a) {
         attend_block_pair<D, FOLD>(sa, sb, nv, lim_a, lim_b, kg, k, v, qa, qb, ident, a.scale_log2);
     };
     if constexpr (LDSK) {
-        // Two K tiles per wave in LDS, double-buffered like the registers.
+        // The walk goes by pairs of key blocks (steps of 32 keys): step t
+        // covers blocks 2t and 2t + 1 (the second past nkb when nkb is odd:
+        // it then contributes nothing). Per step, both K tiles go into the
+        // wave's LDS and both V tiles into registers, double-buffered.
         constexpr int kTileHalfs = D * kBlockTokens;
         constexpr int kDma = kTileHalfs * 2 / (64 * 16);  // 16-byte loads per lane per tile
-        // Two arrays, so the compiler can tell a tile's reads from the other
-        // tile's loads in flight (one array made it wait for those too).
-        __shared__ __align__(16) f16 s_k0[kPrefillWaves * kTileHalfs];
-        __shared__ __align__(16) f16 s_k1[kPrefillWaves * kTileHalfs];
-        f16* const kt0 = s_k0 + w * kTileHalfs;
-        f16* const kt1 = s_k1 + w * kTileHalfs;
-        auto issue_k = [&](int b, f16* dst) {
-            // The tile's previous reads are done (its LDS is rewritten).
-            __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (0x3 << 14));  // lgkmcnt(0)
-            const int bsafe = block_ok(b, a.num_blocks) ? b : 0;
-            const f16* src = a.kc + kv_tile_offset(bsafe, kvh, a.Hkv, D) + 8 * lane;
+        // Two arrays, so the compiler can tell one step's reads from the
+        // other step's loads in flight (one array made it wait for those too).
+        __shared__ __align__(16) f16 s_k0[kPrefillWaves * 2 * kTileHalfs];
+        __shared__ __align__(16) f16 s_k1[kPrefillWaves * 2 * kTileHalfs];
+        f16* const kt0 = s_k0 + w * 2 * kTileHalfs;
+        f16* const kt1 = s_k1 + w * 2 * kTileHalfs;
+        const int nsteps = (nkb + 1) / 2;
+        // Every LDS read of a buffer has been used by an MFMA (so it has
+        // returned) before the buffer is loaded again.
+        auto issue = [&](int b0, int b1, f16* dst, h8 (&vp)[NJ]) {
+            const int bs0 = block_ok(b0, a.num_blocks) ? b0 : 0;
+            const int bs1 = block_ok(b1, a.num_blocks) ? b1 : 0;
+            const f16* k0 = a.kc + kv_tile_offset(bs0, kvh, a.Hkv, D) + 8 * lane;
+            const f16* k1 = a.kc + kv_tile_offset(bs1, kvh, a.Hkv, D) + 8 * lane;
 #pragma unroll
             for (int j = 0; j < kDma; ++j) {
-                __builtin_amdgcn_global_load_lds(src + 512 * j, dst + 512 * j, 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(k0 + 512 * j, dst + 512 * j, 16, 0, 0);
+            }
+#pragma unroll
+            for (int j = 0; j < kDma; ++j) {
+                __builtin_amdgcn_global_load_lds(k1 + 512 * j, dst + kTileHalfs + 512 * j, 16,
+                                                 0, 0);
+            }
+            const f16* v0 = a.vc + kv_tile_offset(bs0, kvh, a.Hkv, D) + loff;
+            const f16* v1 = a.vc + kv_tile_offset(bs1, kvh, a.Hkv, D) + loff;
+#pragma unroll
+            for (int J = 0; J < NJ; ++J) {
+                vp[J] = cat8(load_kv<false>(v0 + kv_elem_offset(16 * J, 0)),
+                             load_kv<false>(v1 + kv_elem_offset(16 * J, 0)));
             }
         };
-        auto load_v = [&](int b, h4 (&v)[NJ]) {
-            const int bsafe = block_ok(b, a.num_blocks) ? b : 0;
-            const f16* vp = a.vc + kv_tile_offset(bsafe, kvh, a.Hkv, D) + loff;
-#pragma unroll
-            for (int J = 0; J < NJ; ++J) v[J] = load_kv<false>(vp + kv_elem_offset(16 * J, 0));
+        // Steps 3 + 4 of step t for both groups. Masks apply only where a
+        // key of the step lies past the wave's first query token (the causal
+        // diagonal; a partial last block and the missing second block of an
+        // odd walk always do) or a block id is out of the pool: a scalar
+        // test. Stale K columns (tokens >= nv) only reach the score rows of
+        // those tokens, which the masks (lim <= nv) replace by -inf.
+        // vw: loads issued after the pair's V loads (std::integral_constant);
+        // the wait for V before PV is explicit, since the compiler's count of
+        // loads into LDS mixed with loads into registers cannot be relied on.
+        auto finish = [&](auto vw, int t, int b0, int b1, f4 (&sc)[4], h8 (&vp)[NJ]) {
+            const int base0 = 2 * t * kBlockTokens;
+            const int base1 = base0 + kBlockTokens;
+            const bool ok0 = block_ok(b0, a.num_blocks);
+            const bool ok1 = (2 * t + 1 < nkb) && block_ok(b1, a.num_blocks);
+            const bool masked = (base0 + 2 * kBlockTokens - 1 > tq0) || !ok0 || !ok1;
+            const int nv0 = ok0 ? min(kBlockTokens, L - base0) : 0;
+            const int nv1 = ok1 ? min(kBlockTokens, L - base1) : 0;
+            const int la0 = ok_a ? min(max(tqa + 1 - base0, 0), nv0) : 0;
+            const int la1 = ok_a ? min(max(tqa + 1 - base1, 0), nv1) : 0;
+            const int lb0 = ok_b ? min(max(tqb + 1 - base0, 0), nv0) : 0;
+            const int lb1 = ok_b ? min(max(tqb + 1 - base1, 0), nv1) : 0;
+            wait_vm<decltype(vw)::value>();
+            mask_v_pair<D>(nv0, nv1, kg, vp);
+            softmax_pv_pair<D, FOLD>(sa, sc[0], sc[2], masked, la0, la1, kg, vp, a.scale_log2);
+            softmax_pv_pair<D, FOLD>(sb, sc[1], sc[3], masked, lb0, lb1, kg, vp, a.scale_log2);
         };
-        // vw: loads issued after v's (std::integral_constant), the V wait.
-        auto attend_l = [&](auto vw, int jb, int b, const f16* kt, h4 (&v)[NJ]) {
-            const int base = jb * kBlockTokens;
-            const int nv = block_ok(b, a.num_blocks) ? min(kBlockTokens, L - base) : 0;
-            const int lim_a = ok_a ? min(max(tqa + 1 - base, 0), nv) : 0;
-            const int lim_b = ok_b ? min(max(tqb + 1 - base, 0), nv) : 0;
-            attend_block_pair_lds<D, FOLD, decltype(vw)::value>(sa, sb, nv, lim_a, lim_b, kg,
-                                                                lane, kt, v, qa, qb,
-                                                                a.scale_log2);
+        // Block ids without scalar loads in the walk (those share their wait
+        // counter with the LDS reads, and every K^T read would wait for
+        // them): chunks of 64 ids (the first slots of blocks 64 c .. 64 c +
+        // 63 of the walk, clamped to block nkb - 1) go into the wave's LDS by
+        // direct loads, chunk c + 1 while the walk is in chunk c, and a step
+        // reads the ids of its two blocks with one LDS read. A chunk is
+        // loaded 64 blocks before its first read; the waits of the steps in
+        // between (each at most 2 * (2 kDma + 2 NJ) loads behind) retire it.
+        __shared__ __align__(16) int s_ids[kPrefillWaves][2][64];
+        auto load_chunk = [&](int c) {
+            const int j = min(64 * c + lane, nkb - 1);
+            __builtin_amdgcn_global_load_lds(srow + j * kBlockTokens, &s_ids[w][c & 1][0], 4, 0,
+                                             0);
         };
-        // Loads in flight behind a block's K tile: its V tile, then the next
-        // block's K tile and V tile (when there is a next block); behind its
-        // V tile, the next block's two tiles or nothing.
-        constexpr int kBehindNext = NJ + kDma + NJ;
-        constexpr int kBehindLast = NJ;
-        const std::integral_constant<int, kDma + NJ> v_next;
+        load_chunk(0);
+        load_chunk(1);
+        __builtin_amdgcn_s_waitcnt(0);
+        int chunk = 0;
+        // Ids of step t's two blocks (steps asked for in increasing order).
+        auto ids_of = [&](int t, int& b0, int& b1) {
+            const int j = min(2 * t, (nkb - 1) & ~1);
+            if ((j >> 6) != chunk) {
+                chunk = j >> 6;
+                load_chunk(chunk + 1);
+            }
+            const int2 v = *reinterpret_cast<const int2*>(&s_ids[w][chunk & 1][j & 63]);
+            b0 = __builtin_amdgcn_readfirstlane(v.x) / kBlockTokens;
+            b1 = __builtin_amdgcn_readfirstlane(v.y) / kBlockTokens;
+        };
+        // Loads in flight behind a step's K tiles: its V tiles, then the next
+        // step's K and V tiles (when there is a next step); behind its V
+        // tiles, the next step's or nothing.
+        constexpr int kBehindNext = 2 * NJ + 2 * kDma + 2 * NJ;
+        constexpr int kBehindLast = 2 * NJ;
+        const std::integral_constant<int, 2 * kDma + 2 * NJ> v_next;
         const std::integral_constant<int, 0> v_last;
-        h4 vA[NJ], vB[NJ];
-        int jA = 0;
-        int bA = block_at(0);
-        int bNext = block_at(min(1, nkb - 1));  // block jA + 1
-        issue_k(bA, kt0);
-        load_v(bA, vA);
-        int left = nkb;
+        h8 vA[NJ], vB[NJ];
+        f4 sc[4];
+        auto qk_then_ids = [&](const f16* kt, int t_ids, int& n0, int& n1) {
+            ids_of(t_ids, n0, n1);
+            qk_pair_lds<D>(sc, lane, kt, qa, qb);
+        };
+        int tA = 0;
+        int bA0, bA1, bN0, bN1;  // step tA, step tA + 1 (clamped)
+        ids_of(0, bA0, bA1);
+        ids_of(1, bN0, bN1);
+        issue(bA0, bA1, kt0, vA);
+        int left = nsteps;
         for (; left > 2; left -= 2) {
-            const int jB = jA + 1;
-            const int bB = bNext;
-            issue_k(bB, kt1);
-            load_v(bB, vB);
-            bNext = block_at(jB + 1);
+            const int tB = tA + 1;
+            const int bB0 = bN0, bB1 = bN1;
+            issue(bB0, bB1, kt1, vB);
             wait_vm<kBehindNext>();
-            attend_l(v_next, jA, bA, kt0, vA);
-            jA = jB + 1;
-            bA = bNext;
-            issue_k(bA, kt0);
-            load_v(bA, vA);
-            bNext = block_at(min(jA + 1, nkb - 1));
+            qk_then_ids(kt0, tB + 1, bN0, bN1);
+            finish(v_next, tA, bA0, bA1, sc, vA);
+            tA = tB + 1;
+            bA0 = bN0;
+            bA1 = bN1;
+            issue(bA0, bA1, kt0, vA);
             wait_vm<kBehindNext>();
-            attend_l(v_next, jB, bB, kt1, vB);
+            qk_then_ids(kt1, tA + 1, bN0, bN1);
+            finish(v_next, tB, bB0, bB1, sc, vB);
         }
         if (left == 2) {
-            const int jB = jA + 1;
-            const int bB = bNext;
-            issue_k(bB, kt1);
-            load_v(bB, vB);
+            const int tB = tA + 1;
+            issue(bN0, bN1, kt1, vB);
             wait_vm<kBehindNext>();
-            attend_l(v_next, jA, bA, kt0, vA);
+            qk_pair_lds<D>(sc, lane, kt0, qa, qb);
+            finish(v_next, tA, bA0, bA1, sc, vA);
             wait_vm<kBehindLast>();
-            attend_l(v_last, jB, bB, kt1, vB);
+            qk_pair_lds<D>(sc, lane, kt1, qa, qb);
+            finish(v_last, tB, bN0, bN1, sc, vB);
         } else {
             wait_vm<kBehindLast>();
-            attend_l(v_last, jA, bA, kt0, vA);
+            qk_pair_lds<D>(sc, lane, kt0, qa, qb);
+            finish(v_last, tA, bA0, bA1, sc, vA);
         }
         // No load may still be writing this wave's LDS when it exits.
         __builtin_amdgcn_s_waitcnt(0);

@@ -58,6 +58,16 @@ def test_prefill_long_prompts(dev, entry):
     assert_attention_close(_run(w, entry), _ref(w), f"prefill long {entry}")
 
 
+@pytest.mark.parametrize("H,Hkv,D", [(32, 8, 128), (16, 4, 64)])
+def test_prefill_walks_past_two_id_chunks(dev, H, Hkv, D):
+    """Key walks of more than 128 blocks: the kernel keeps the block ids of
+    its walk in chunks of 64 blocks, double-buffered, so a 2600-token prompt
+    crosses into the second chunk and reuses the first chunk's buffer for the
+    third; 1100 tokens end just past the first chunk; 5 is a one-block walk."""
+    w = workloads.prefill_config((2600, 1100, 5), H, Hkv, D, seed=21 + D)
+    assert_attention_close(_run(w), _ref(w), f"prefill id chunks H{H} Hkv{Hkv} D{D}")
+
+
 @pytest.mark.parametrize("scale", [-0.0883883, 0.0, 0.3])
 def test_prefill_scale_signs(dev, scale):
     """A positive scale takes the kernel's path with the scale folded into the
