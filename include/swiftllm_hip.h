@@ -211,7 +211,8 @@ int swiftllm_hip_reshape_and_cache(const void* key, const void* value,
  * before it. Token i of s attends to tokens j <= i of s, whose K/V sit in
  * the cache at slot_mapping[start_s + j]; the slots of a sequence must walk
  * its block table from position 0 (table[p / 16] * 16 + p % 16).
- * params->max_context_len bounds every context_lens[s]. */
+ * params->max_context_len bounds every context_lens[s]; above 2^24 tokens it
+ * can return SWIFTLLM_ERR_NOT_SUPPORTED (grid size). */
 int swiftllm_hip_paged_attention_prefill(
     void* output, const void* query, const void* key_cache,
     const void* value_cache, const int32_t* slot_mapping,

@@ -58,6 +58,7 @@ struct PrefillArgs {
     int gw;              // query heads per row group: min(G, 16)
     int tpw;             // query tokens per row group: 16 / gw (a wave has two groups)
     int groups;          // workgroups per (sequence, kv head chunk) in the grid
+    long long units;     // (sequence, kv head chunk) pairs: S * Hkv * nhc
     int num_blocks;      // bound on block ids; <= 0: unbounded
 };
 
@@ -215,10 +216,23 @@ void paged_prefill_kernel(const PrefillArgs a) {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15;
     const int kg = lane >> 4;
-    const int s = blockIdx.z;
-    const int kvh = blockIdx.y / a.nhc;
-    const int hc = blockIdx.y - kvh * a.nhc;
-    const int gi = a.groups - 1 - static_cast<int>(blockIdx.x);  // latest tokens first
+    // Workgroups are dealt to the 8 XCDs round-robin in launch order (x
+    // fastest), so blockIdx.x % 8 names the XCD. XCD x takes the units
+    // (sequence, kv head chunk) x, x + 8, x + 16, ... one after the other,
+    // each unit's groups latest tokens first: the workgroups an XCD runs at
+    // one time share one unit's K/V in that XCD's L2, and every XCD gets
+    // the same kv heads of every sequence (equal work for any lengths when
+    // the kv heads divide over the XCDs).
+    const long long round =
+        static_cast<long long>(blockIdx.y) + static_cast<long long>(gridDim.y) * blockIdx.z;
+    const long long unit = static_cast<long long>(blockIdx.x & 7) + 8 * round;
+    if (unit >= a.units) return;  // the whole workgroup: no barrier is skipped
+    const int per_seq = a.Hkv * a.nhc;
+    const int s = static_cast<int>(unit / per_seq);
+    const int yy = static_cast<int>(unit - static_cast<long long>(s) * per_seq);
+    const int kvh = yy / a.nhc;
+    const int hc = yy - kvh * a.nhc;
+    const int gi = a.groups - 1 - static_cast<int>(blockIdx.x >> 3);  // latest tokens first
 
     // start_s = sum of the lengths before s (all threads share the sum).
     int part = 0;
@@ -531,10 +545,21 @@ int prefill(const char* who, void* out, const void* q, const void* kc, const voi
     a.gw = a.G < 16 ? a.G : 16;
     a.tpw = 16 / a.gw;
     const long long per_wg = static_cast<long long>(kPrefillWaves) * 2 * a.tpw;
-    a.groups = static_cast<int>((max_len + per_wg - 1) / per_wg);
+    const long long groups = (max_len + per_wg - 1) / per_wg;
+    // x = 8 * groups workgroups of 64 * kPrefillWaves threads must stay
+    // below 2^32 threads.
+    if (groups >= (1LL << 21)) {
+        return fail(SWIFTLLM_ERR_NOT_SUPPORTED,
+                    "%s: max_context_len=%lld needs %lld workgroups per sequence (limit 2^21)", who,
+                    max_len, groups);
+    }
+    a.groups = static_cast<int>(groups);
+    a.units = S * static_cast<long long>(a.Hkv) * a.nhc;
     a.num_blocks = num_blocks;
-    const dim3 grid(static_cast<unsigned>(a.groups), static_cast<unsigned>(a.Hkv * a.nhc),
-                    static_cast<unsigned>(S));
+    const long long rounds = (a.units + 7) / 8;
+    const long long gy = rounds < 65535 ? rounds : 65535;
+    const dim3 grid(static_cast<unsigned>(8 * a.groups), static_cast<unsigned>(gy),
+                    static_cast<unsigned>((rounds + gy - 1) / gy));
     const dim3 block(64 * kPrefillWaves);
     const bool fold = a.scale_log2 > 0.0f;
     const bool ldsk = aligned(kc, 16);
