@@ -526,6 +526,17 @@ int prefill(const char* who, void* out, const void* q, const void* kc, const voi
         !aligned(slots, 4) || !aligned(ctx, 4)) {
         return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: misaligned pointer", who);
     }
+    // Workgroups per (sequence, kv head chunk): x = 8 of them per XCD round
+    // times 64 * kPrefillWaves threads must stay below 2^32 threads.
+    const long long G = H / Hkv;
+    const long long tpw = 16 / (G < 16 ? G : 16);
+    const long long per_wg = static_cast<long long>(kPrefillWaves) * 2 * tpw;
+    const long long groups = (max_len + per_wg - 1) / per_wg;
+    if (groups >= (1LL << 21)) {
+        return fail(SWIFTLLM_ERR_NOT_SUPPORTED,
+                    "%s: max_context_len=%lld needs %lld workgroups per sequence (limit 2^21)", who,
+                    max_len, groups);
+    }
     int rc = require_device();
     if (rc != SWIFTLLM_OK) return rc;
     if (S == 0 || max_len == 0) return ok();
@@ -544,15 +555,6 @@ int prefill(const char* who, void* out, const void* q, const void* kc, const voi
     a.nhc = (a.G + 15) / 16;
     a.gw = a.G < 16 ? a.G : 16;
     a.tpw = 16 / a.gw;
-    const long long per_wg = static_cast<long long>(kPrefillWaves) * 2 * a.tpw;
-    const long long groups = (max_len + per_wg - 1) / per_wg;
-    // x = 8 * groups workgroups of 64 * kPrefillWaves threads must stay
-    // below 2^32 threads.
-    if (groups >= (1LL << 21)) {
-        return fail(SWIFTLLM_ERR_NOT_SUPPORTED,
-                    "%s: max_context_len=%lld needs %lld workgroups per sequence (limit 2^21)", who,
-                    max_len, groups);
-    }
     a.groups = static_cast<int>(groups);
     a.units = S * static_cast<long long>(a.Hkv) * a.nhc;
     a.num_blocks = num_blocks;

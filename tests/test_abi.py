@@ -153,6 +153,26 @@ def test_expert_gemm_validation():
     assert gemm(FAKE, None, None, FAKE, 8, 64, 4096, 4096, FAKE, None) == INVALID
 
 
+def test_prefill_validation():
+    """Prefill arguments refused before any device work: head_dim other than
+    64 / 128, heads not a multiple of kv heads, a negative length, a null
+    pointer, and a max_context_len whose grid would need 2^21 or more
+    workgroups per sequence (G = 4: 32 query tokens per workgroup)."""
+    L = _lib.lib()
+
+    def call(S=2, H=32, Hkv=8, D=128, max_len=64, q=FAKE):
+        return L.swiftllm_hip_launch_paged_prefill(FAKE, q, FAKE, FAKE, FAKE, FAKE, 0.1, S, H,
+                                                   Hkv, D, 16, max_len, 0, None)
+
+    assert call(D=96) == UNSUP
+    assert call(H=30) == INVALID
+    assert call(max_len=-1) == INVALID
+    assert call(q=None) == INVALID
+    assert call(max_len=32 << 21) == UNSUP
+    # Just under the limit passes validation (no sequences: nothing launches).
+    assert call(S=0, max_len=(32 << 21) - 32) in (OK, NODEV)
+
+
 @pytest.mark.skipif(_hip.device_count() > 0, reason="checks the no-device path")
 def test_device_not_found_without_gpu():
     """Valid arguments on a host without a HIP device: DeviceNotFound, the
