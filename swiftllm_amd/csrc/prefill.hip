@@ -28,8 +28,10 @@
 // step shared with decode (attention_core.hpp: an identity-MFMA
 // transposition of K in registers). A wave's rows are complete when
 // its walk ends, so it writes its outputs directly: no combine, no barriers.
-// Four waves per workgroup take consecutive token groups; workgroups go out
-// latest tokens first (the longest walks start first). K/V tiles are loaded
+// Four waves per workgroup take consecutive token groups. Each XCD runs the
+// (sequence, kv head) units of its residue mod 8 one after the other, each
+// unit's workgroups latest tokens first (the longest walks start first), so
+// the workgroups resident on an XCD share one unit's K/V in its L2. K/V tiles are loaded
 // with ordinary (cached) loads: every query group of a sequence re-reads them.
 
 #include <type_traits>
