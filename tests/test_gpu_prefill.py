@@ -105,6 +105,33 @@ def test_prefill_empty_and_zero_length_sequences(dev):
     assert_attention_close(out, _ref(w), "prefill with empty prompts")
 
 
+def test_prefill_grid_rounds_past_65535(dev):
+    """65535 one-token prompts with 16 kv heads: 1,048,560 (sequence, kv head)
+    units, so the launch needs 131,070 rounds of 8 units, more than one grid
+    row (65535) holds, and the second grid plane runs. A one-token prompt
+    attends only to itself: out = its own V (the prompts share a pool of 64
+    blocks; slots 1..15 of every block hold NaN)."""
+    S, H, Hkv, D, NB = 65535, 16, 16, 64, 64
+    rng = np.random.default_rng(5)
+    q = (rng.standard_normal((S, H, D)) * 0.5).astype(np.float16)
+    kc = np.full((NB, Hkv, D, 16), np.nan, np.float16)
+    vc = np.full((NB, Hkv, D, 16), np.nan, np.float16)
+    kc[:, :, :, 0] = (rng.standard_normal((NB, Hkv, D)) * 0.5).astype(np.float16)
+    vc[:, :, :, 0] = (rng.standard_normal((NB, Hkv, D)) * 0.5).astype(np.float16)
+    block = np.arange(S, dtype=np.int32) % NB
+    slots = (block * 16).astype(np.int32)
+    ctx = np.ones(S, np.int32)
+    out = DeviceArray((S, H, D), np.float16)
+    out.fill_byte(0xFF)
+    pa.launch_paged_prefill(out, DeviceArray.from_numpy(q), DeviceArray.from_numpy(kc),
+                            DeviceArray.from_numpy(vc), DeviceArray.from_numpy(slots),
+                            DeviceArray.from_numpy(ctx), 1.0 / 8.0, S, H, Hkv, D, 16, 1,
+                            num_blocks=NB)
+    synchronize()
+    expect = vc[block, :, :, 0]  # [S, Hkv, D]; G = 1: head h reads kv head h
+    assert_attention_close(out.numpy(), expect, "prefill 65535 one-token prompts")
+
+
 def test_prefill_max_len_above_every_prompt(dev):
     """A generous max_context_len only adds workgroups that exit at once."""
     w = workloads.prefill_config((20, 50), 8, 2, 64, seed=9)
