@@ -545,9 +545,9 @@ def bench_moe_mlp(args):
     """Config 8: the whole Mixtral-8x7B MoE layer after the router: top-2 of
     8 experts for 4096 tokens (config 5's inputs), the gated expert GEMM
     (hidden 4096 -> 2 x 14336 with SiLU * up fused), the down GEMM
-    (14336 -> 4096) and the weighted combine. Weights are random fp16, one
-    random matrix per projection copied to every expert on the device."""
-    from swiftllm_amd import _hip, moe, workloads
+    (14336 -> 4096) and the weighted combine. Weights are random fp16 and
+    differ between experts (workloads.expert_weights)."""
+    from swiftllm_amd import moe, workloads
     from swiftllm_amd._hip import DeviceArray, Stream
 
     wl = workloads.moe_config(seed=args.seed)
@@ -557,14 +557,7 @@ def bench_moe_mlp(args):
     stream = Stream()
 
     def stacked(n, k):
-        one = (rng.standard_normal((n, k), dtype=np.float32) / np.sqrt(k)).astype(np.float16)
-        d = DeviceArray((E, n, k), np.float16)
-        src = DeviceArray.from_numpy(one)
-        for e in range(E):
-            _hip.check(_hip.hip().hipMemcpy(d.ptr + e * one.nbytes, src.ptr, one.nbytes,
-                                            _hip.HIP_MEMCPY_D2D), "weight copy")
-        src.free()
-        return d
+        return DeviceArray.from_numpy(workloads.expert_weights(rng, E, n, k))
 
     wg, wu, wd = stacked(I, hidden), stacked(I, hidden), stacked(hidden, I)
     mlp = moe.MoeMlp(E, K, wg, wu, wd)

@@ -117,6 +117,10 @@ int swiftllm_hip_pack_block_tables(const uint64_t* block_ids,
         return fail(SWIFTLLM_ERR_INVALID_PARAMETER,
                     "max_blocks_per_seq does not fit in int32");
     }
+    // block_ids may be null only when every table is empty.
+    if (!block_ids && table_offsets[num_seqs] != table_offsets[0]) {
+        return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "null block_ids");
+    }
     for (size_t s = 0; s < num_seqs; ++s) {
         const uint64_t begin = table_offsets[s];
         const uint64_t end = table_offsets[s + 1];

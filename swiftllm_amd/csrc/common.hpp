@@ -56,6 +56,11 @@ hipError_t launch(void (*kernel)(Args), dim3 grid, dim3 block, size_t lds,
 // contiguous tile of head_dim rows of 16 tokens.
 // ---------------------------------------------------------------------------
 constexpr int kBlockTokens = 16;
+// slot >> kBlockShift is the block of a slot. The arithmetic shift keeps a
+// negative slot (padding) negative, where slot / 16 would truncate -1..-15
+// to block 0.
+constexpr int kBlockShift = 4;
+static_assert((1 << kBlockShift) == kBlockTokens, "block shift");
 
 __host__ __device__ inline size_t kv_tile_offset(int block, int kv_head,
                                                  int num_kv_heads,

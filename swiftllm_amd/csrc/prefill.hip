@@ -298,7 +298,7 @@ void paged_prefill_kernel(const PrefillArgs a) {
     // last one or two are peeled off.
     const int nkb = tq_last / kBlockTokens + 1;
     auto block_at = [&](int jb) {
-        return __builtin_amdgcn_readfirstlane(srow[jb * kBlockTokens]) / kBlockTokens;
+        return __builtin_amdgcn_readfirstlane(srow[jb * kBlockTokens]) >> kBlockShift;
     };
     auto attend = [&](int jb, int b, h4 (&k)[NJ], h4 (&v)[NJ]) {
         const int base = jb * kBlockTokens;
@@ -397,8 +397,8 @@ void paged_prefill_kernel(const PrefillArgs a) {
                 load_chunk(chunk + 1);
             }
             const int2 v = *reinterpret_cast<const int2*>(&s_ids[w][chunk & 1][j & 63]);
-            b0 = __builtin_amdgcn_readfirstlane(v.x) / kBlockTokens;
-            b1 = __builtin_amdgcn_readfirstlane(v.y) / kBlockTokens;
+            b0 = __builtin_amdgcn_readfirstlane(v.x) >> kBlockShift;
+            b1 = __builtin_amdgcn_readfirstlane(v.y) >> kBlockShift;
         };
         // Loads in flight behind a step's K tiles: its V tiles, then the next
         // step's K and V tiles (when there is a next step); behind its V

@@ -219,3 +219,17 @@ def moe_config(seed: int = 0, *, num_tokens: int = 4096, hidden: int = 4096,
     x = _normal_f16(rng, (num_tokens, hidden), 1.0)
     logits = rng.standard_normal((num_tokens, num_experts), dtype=np.float32)
     return MoeWorkload(x=x, logits=logits, top_k=top_k)
+
+
+def expert_weights(rng: np.random.Generator, num_experts: int, n: int, k: int) -> np.ndarray:
+    """fp16 [E, n, k] Linear weights (rows = output features), a different
+    matrix for every expert: one N(0, 1/k) matrix whose rows each expert
+    takes in its own seeded order. Expert e's output column j is then
+    column perm_e[j] of the shared matrix, so a tile computed with another
+    expert's weight, or with the right weight at the wrong rows, gives
+    different values."""
+    base = _normal_f16(rng, (n, k), 1.0 / math.sqrt(k))
+    out = np.empty((num_experts, n, k), np.float16)
+    for e in range(num_experts):
+        np.take(base, rng.permutation(n), axis=0, out=out[e])
+    return out

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 import oracle
-from swiftllm_amd import moe
+from swiftllm_amd import moe, workloads
 from swiftllm_amd._hip import DeviceArray, synchronize
 
 pytestmark = pytest.mark.gpu
@@ -106,3 +106,71 @@ def test_moe_mlp_chain(dev):
     y = oracle.moe_expert_gemm(h, wd, None, offsets).astype(np.float16)
     ref = oracle.moe_combine(y, w.astype(np.float32), inverse)
     _close(out.numpy().astype(np.float64), ref, "moe mlp")
+
+
+def _sample_rows(rng, offs, tile=256, per_tile=2):
+    """Rows to check against the float64 oracle: for every expert with rows,
+    its first and last row and `per_tile` random rows of each 256-row tile,
+    so every (row tile, column tile) pair of the grid is covered."""
+    rows = []
+    for e in range(len(offs) - 1):
+        r0, r1 = int(offs[e]), int(offs[e + 1])
+        if r1 <= r0:
+            continue
+        rows += [r0, r1 - 1]
+        for t0 in range(r0, r1, tile):
+            t1 = min(t0 + tile, r1)
+            rows += [int(x) for x in rng.integers(t0, t1, per_tile)]
+    return np.unique(np.array(rows, np.int64))
+
+
+@pytest.mark.parametrize("gated,n,k", [(True, 14336, 4096), (False, 4096, 14336)])
+def test_expert_gemm_mixtral_size(dev, gated, n, k):
+    """The sizes bench config 8 runs (Mixtral-8x7B layer, 4096 tokens top-2):
+    gated k 4096 -> n 14336 and down k 14336 -> n 4096 over m_total 8192
+    rows in 8 uneven experts, expert 5 empty, a different weight for every
+    expert. That is 56 / 16 column tiles, the 64- and 224-step k loops and
+    the XCD super-tile remap over hundreds of tiles, none of which the small
+    shapes reach.
+
+    Checks: every output is written (the output starts as NaN); sampled rows
+    from every row tile, all n columns, against the float64 oracle; and for
+    the plain GEMM every row through a random-sign projection:
+    c_row . v = a_row . (W_e^T v) exactly, and the rounding of the n fp16
+    outputs (each within 2^-11 of its value) moves c_row . v by a Rademacher
+    sum of standard deviation <= 2^-11 ||c_row||, held to 7 of those (plus
+    the fp32 accumulation) where one wrong element moves it by O(rms)."""
+    E, m_total = 8, 8192
+    rng = np.random.default_rng(8 + gated)
+    offs = _offsets(rng, E, m_total, empty=(5,))
+    a = workloads._normal_f16(rng, (m_total, k), 0.5)
+    w = workloads.expert_weights(rng, E, n, k)
+    w2 = workloads.expert_weights(rng, E, n, k) if gated else None
+    c = DeviceArray((m_total, n), np.float16)
+    c.fill_byte(0xFF)
+    moe.moe_expert_gemm(DeviceArray.from_numpy(a), DeviceArray.from_numpy(w),
+                        DeviceArray.from_numpy(w2) if gated else None,
+                        DeviceArray.from_numpy(offs), c)
+    synchronize()
+    got = c.numpy()
+    assert np.isfinite(got).all(), "an output was not written (still NaN)"
+
+    rows = _sample_rows(rng, offs)
+    sub_counts = [int(((rows >= offs[e]) & (rows < offs[e + 1])).sum()) for e in range(E)]
+    sub_offs = np.concatenate([[0], np.cumsum(sub_counts)]).astype(np.int32)
+    ref = oracle.moe_expert_gemm(a[rows], w, w2, sub_offs)
+    _close(got[rows].astype(np.float64), ref, f"gemm gated={gated} n{n} k{k} sampled rows")
+
+    if not gated:
+        v = rng.choice([-1.0, 1.0], size=n)
+        g = got.astype(np.float64)
+        lhs = g @ v
+        rms = float(np.sqrt(np.mean(ref ** 2)))
+        for e in range(E):
+            r0, r1 = int(offs[e]), int(offs[e + 1])
+            if r1 <= r0:
+                continue
+            rhs = a[r0:r1].astype(np.float64) @ (w[e].astype(np.float64).T @ v)
+            sigma = 2.0 ** -11 * np.linalg.norm(g[r0:r1], axis=1) + 1e-4 * rms * np.sqrt(n)
+            worst = float((np.abs(lhs[r0:r1] - rhs) - 7 * sigma).max())
+            assert worst <= 0, f"expert {e}: projection off by {worst:.3e} beyond 7 sigma"

@@ -150,6 +150,37 @@ def test_prefill_out_of_pool_blocks_are_skipped(dev):
     assert np.all(np.isfinite(out[40:].astype(np.float64)))
 
 
+@pytest.mark.parametrize("key_offset", [0, 8])
+def test_prefill_padding_slots_attend_nothing(dev, key_offset):
+    """A prompt whose slots are -1 (padding, as reshape_and_cache skips them)
+    reads no block: -1 // 16 must not become block 0. Its rows attend to no
+    key and come out as zeros; the prompts beside it are exact. key_offset 8
+    runs the register path for K, 0 the LDS path."""
+    w = workloads.prefill_config((40, 24, 19), 8, 2, 64, seed=12)
+    w.slot_mapping[40:64] = -1
+    T, H, D = w.q.shape
+    S = len(w.context_lens)
+    kc_buf = DeviceArray((w.key_cache.nbytes + 16,), np.uint8)
+    kc_bytes = np.zeros(w.key_cache.nbytes + 16, np.uint8)
+    kc_bytes[key_offset:key_offset + w.key_cache.nbytes] = w.key_cache.view(np.uint8).ravel()
+    kc_buf.upload(kc_bytes)
+    out = DeviceArray((T, H, D), np.float16)
+    out.fill_byte(0xFF)
+    sm, ctx = DeviceArray.from_numpy(w.slot_mapping), DeviceArray.from_numpy(w.context_lens)
+    pa.launch_paged_prefill(out, DeviceArray.from_numpy(w.q), kc_buf.ptr + key_offset,
+                            DeviceArray.from_numpy(w.value_cache), sm, ctx, w.scale, S, H, 2, D, 16,
+                            int(w.context_lens.max()), num_blocks=w.key_cache.shape[0])
+    synchronize()
+    got = out.numpy()
+    assert np.array_equal(got[40:64].view(np.uint16), np.zeros((24, H, D), np.uint16))
+    ref_a = oracle.prefill_numpy(w.q[:40], w.key_cache, w.value_cache, w.slot_mapping[:40],
+                                 w.context_lens[:1], w.scale)
+    ref_c = oracle.prefill_numpy(w.q[64:], w.key_cache, w.value_cache, w.slot_mapping[64:],
+                                 w.context_lens[2:], w.scale)
+    assert_attention_close(got[:40], ref_a, "prefill prompt before the padding")
+    assert_attention_close(got[64:], ref_c, "prefill prompt after the padding")
+
+
 def _ref_first(w, n):
     return oracle.prefill_numpy(w.q[:n], w.key_cache, w.value_cache, w.slot_mapping[:n],
                                 w.context_lens[:1], w.scale)

@@ -124,6 +124,27 @@ def test_pack_block_tables_errors():
         batch.pack(16, max_blocks_per_seq=2)
 
 
+def test_pack_block_tables_null_block_ids():
+    """A null block_ids with a non-empty table is refused, not dereferenced;
+    with every table empty it is accepted (nothing is read)."""
+    from swiftllm_amd import _lib
+
+    L = _lib.lib()
+    offs = np.array([0, 2], np.uint64)
+    ctx = np.array([20], np.uint64)
+    bt = np.zeros((1, 4), np.int32)
+    cl = np.zeros(1, np.int32)
+    rc = L.swiftllm_hip_pack_block_tables(None, offs.ctypes.data, ctx.ctypes.data, 1, 16, 4,
+                                          bt.ctypes.data, cl.ctypes.data)
+    assert rc == pa.InvalidParameter.code
+    assert "block_ids" in _lib.last_error()[1]
+    offs0 = np.array([0, 0], np.uint64)
+    ctx0 = np.array([0], np.uint64)
+    rc = L.swiftllm_hip_pack_block_tables(None, offs0.ctypes.data, ctx0.ctypes.data, 1, 16, 4,
+                                          bt.ctypes.data, cl.ctypes.data)
+    assert rc == 0 and cl[0] == 0 and not bt.any()
+
+
 def test_pack_block_tables_random():
     rng = np.random.default_rng(0)
     batch = pa.BatchedCacheMetadata()
