@@ -5,7 +5,9 @@
  *
  * Every entry point:
  *   - takes caller-owned device pointers on the current HIP device;
- *   - allocates nothing (scratch memory is passed in by the caller);
+ *   - allocates nothing (scratch memory is passed in by the caller, except
+ *     for swiftllm_hip_launch_paged_attention_v2_noalloc, whose scratch is a
+ *     static device array);
  *   - is asynchronous on the given stream (NULL = the default stream);
  *   - validates its arguments synchronously on the host before any launch.
  *
@@ -159,6 +161,27 @@ int swiftllm_hip_launch_reshape_and_cache(
     const void* key, const void* value, void* key_cache, void* value_cache,
     const int* slot_mapping, int num_tokens, int num_kv_heads, int head_dim,
     int block_size, int num_blocks, hipStream_t stream);
+
+/* Bytes of the static device scratch behind
+ * swiftllm_hip_launch_paged_attention_v2_noalloc (one copy per device). */
+#define SWIFTLLM_HIP_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): swiftllm_hip_launch_paged_attention_v2 without the
+ * workspace arguments. Its split-K scratch is a static device array of
+ * SWIFTLLM_HIP_NOALLOC_SCRATCH_BYTES bytes that each device holds from its
+ * first call until the process ends; nothing is allocated or freed per call.
+ * Sizes whose workspace (swiftllm_hip_paged_attention_v2_workspace_size for
+ * the mode the call runs) exceeds that return SWIFTLLM_ERR_INVALID_PARAMETER.
+ * All calls on one device share the array: calls that overlap on a device
+ * (several streams or host threads) race and must be ordered on one stream. */
+int swiftllm_hip_launch_paged_attention_v2_noalloc(
+    void* output, const void* query, const void* key_cache,
+    const void* value_cache, const int* block_tables, const int* context_lens,
+    float scale, int num_seqs, int num_heads, int num_kv_heads, int head_dim,
+    int block_size, int max_num_blocks_per_seq, int partition_size,
+    int num_blocks, hipStream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* 3. Params-struct twins of crates/swiftllm-cuda/src/bindings.rs.           */

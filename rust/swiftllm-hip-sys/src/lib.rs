@@ -34,6 +34,9 @@ pub const SWIFTLLM_ERR_INVALID_PARAMETER: c_int = -4;
 pub const SWIFTLLM_ERR_DEVICE_NOT_FOUND: c_int = -5;
 pub const SWIFTLLM_ERR_NOT_SUPPORTED: c_int = -6;
 
+/// SWIFTLLM_HIP_NOALLOC_SCRATCH_BYTES: the static split-K scratch per device.
+pub const SWIFTLLM_HIP_NOALLOC_SCRATCH_BYTES: usize = 64 << 20;
+
 /// C twin of `PagedAttentionParams` (crates/swiftllm-cuda/src/bindings.rs:8-30).
 #[repr(C)]
 #[derive(Debug, Clone, Copy)]
@@ -115,6 +118,18 @@ extern "C" {
         value_cache: *mut c_void, slot_mapping: *const c_int, num_tokens: c_int,
         num_kv_heads: c_int, head_dim: c_int, block_size: c_int, num_blocks: c_int,
         stream: hipStream_t,
+    ) -> c_int;
+
+    /// No counterpart in the reference: split-K decode for callers that cannot
+    /// allocate (graph capture, tight serving loops), with its scratch in a
+    /// static device array of SWIFTLLM_HIP_NOALLOC_SCRATCH_BYTES per device.
+    /// Calls that overlap on one device race on that array.
+    pub fn swiftllm_hip_launch_paged_attention_v2_noalloc(
+        output: *mut c_void, query: *const c_void, key_cache: *const c_void,
+        value_cache: *const c_void, block_tables: *const c_int, context_lens: *const c_int,
+        scale: c_float, num_seqs: c_int, num_heads: c_int, num_kv_heads: c_int,
+        head_dim: c_int, block_size: c_int, max_num_blocks_per_seq: c_int,
+        partition_size: c_int, num_blocks: c_int, stream: hipStream_t,
     ) -> c_int;
 
     // -- params-struct twins of bindings.rs ------------------------------------

@@ -12,6 +12,9 @@ LIB_PATH = Path(__file__).resolve().parent / "libswiftllm_hip.so"
 
 _LIB: Optional[ctypes.CDLL] = None
 
+# SWIFTLLM_HIP_NOALLOC_SCRATCH_BYTES of include/swiftllm_hip.h.
+NOALLOC_SCRATCH_BYTES = 64 << 20
+
 vp = ctypes.c_void_p
 i32 = ctypes.c_int
 sz = ctypes.c_size_t
@@ -61,6 +64,8 @@ SIGNATURES = {
     "swiftllm_hip_launch_paged_attention_v2": (
         i32, [vp, vp, sz, vp, vp, vp, vp, vp, f32, i32, i32, i32, i32, i32, i32, i32, i32, vp]),
     "swiftllm_hip_launch_reshape_and_cache": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]),
+    "swiftllm_hip_launch_paged_attention_v2_noalloc": (
+        i32, [vp, vp, vp, vp, vp, vp, f32, i32, i32, i32, i32, i32, i32, i32, i32, vp]),
     "swiftllm_hip_paged_attention_decode": (
         i32, [vp, vp, vp, vp, vp, vp, ctypes.POINTER(PagedAttentionParams), vp]),
     "swiftllm_hip_reshape_and_cache": (

@@ -37,6 +37,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 
 #include "attention_core.hpp"
 
@@ -1131,19 +1132,30 @@ int decode_balanced(void* out, void* ws, size_t ws_bytes, const void* q, const v
     return launched(err, who);
 }
 
+// The partition size a v2 call runs with: balanced mode (0) needs its
+// prefix table in LDS and at least 4 teams of Hkv * nhc waves; otherwise it
+// falls back to partitions of 512 tokens.
+int effective_partition(const Shape& sh, int partition_size, int cus) {
+    if (partition_size == 0 &&
+        (sh.S > kStreamMaxSeqs ||
+         static_cast<long long>(sh.Hkv) * ((sh.H / sh.Hkv + 15) / 16) * 4 > cus * kStreamWavesPerCU)) {
+        return 512;
+    }
+    return partition_size;
+}
+
+// Workspace bytes a v2 call with this (effective) partition size uses.
+size_t v2_bytes(const Shape& sh, int partition_size, int cus) {
+    return partition_size == 0 ? stream_need(sh, cus).total : v2_need(sh, partition_size).total;
+}
+
 int decode_v2(void* out, void* ws, size_t ws_bytes, const void* q, const void* kc, const void* vc,
               const int* bt, const int* ctx, float scale, const Shape& sh, int partition_size,
               int num_blocks, hipStream_t stream, const char* who) {
     int rc = validate_decode(who, out, q, kc, vc, bt, ctx, sh);
     if (rc != SWIFTLLM_OK) return rc;
     if ((rc = validate_partition(who, partition_size)) != SWIFTLLM_OK) return rc;
-    // Balanced mode needs its prefix table in LDS and at least 4 teams of
-    // Hkv * nhc waves; otherwise it falls back to partitions of 512 tokens.
-    if (partition_size == 0 &&
-        (sh.S > kStreamMaxSeqs ||
-         static_cast<long long>(sh.Hkv) * ((sh.H / sh.Hkv + 15) / 16) * 4 > device_cus() * kStreamWavesPerCU)) {
-        partition_size = 512;
-    }
+    partition_size = effective_partition(sh, partition_size, device_cus());
     if (partition_size == 0) {
         if (sh.S > 0 && (ws == nullptr || !aligned(ws, 256))) {
             return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: workspace null or not 256-byte aligned", who);
@@ -1196,6 +1208,77 @@ int decode_v2(void* out, void* ws, size_t ws_bytes, const void* q, const void* k
 }  // namespace
 }  // namespace swiftllm
 
+// ---------------------------------------------------------------------------
+// Split-K decode with no allocation. Some callers cannot allocate (code under
+// HIP graph capture, tight serving loops, harnesses that forbid hipMalloc),
+// so swiftllm_hip_launch_paged_attention_v2_noalloc takes its workspace from
+// this static device array instead of an argument. Each device that loads the
+// library holds its own copy until the process ends. All calls on a device
+// share that copy: calls that overlap on one device (several streams or host
+// threads) race on it and must be ordered on one stream. The split-K
+// workspace is plain scratch (a call reads only what it wrote first), so
+// nothing is cleared between calls.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[SWIFTLLM_HIP_NOALLOC_SCRATCH_BYTES];
+
+namespace swiftllm {
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on the current device, looked up on the first
+// call on that device. In host code the array's name is only a host-side
+// stand-in; this address is what kernels receive.
+int static_scratch(void** ptr, const char* who) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        return fail(SWIFTLLM_ERR_DEVICE_NOT_FOUND, "%s: no current HIP device", who);
+    }
+    if (dev < 0 || dev >= kMaxScratchDevices) {
+        return fail(SWIFTLLM_ERR_NOT_SUPPORTED, "%s: device %d beyond the %d the library tracks", who,
+                    dev, kMaxScratchDevices);
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || p == nullptr) {
+            return fail(SWIFTLLM_ERR_INIT, "%s: hipGetSymbolAddress(scratch) on device %d: %s", who, dev,
+                        hipGetErrorString(err));
+        }
+        g_scratch[dev] = p;
+    }
+    *ptr = g_scratch[dev];
+    return SWIFTLLM_OK;
+}
+
+int decode_v2_noalloc(void* out, const void* q, const void* kc, const void* vc, const int* bt,
+                      const int* ctx, float scale, const Shape& sh, int partition_size,
+                      int num_blocks, hipStream_t stream, const char* who) {
+    int rc = validate_decode(who, out, q, kc, vc, bt, ctx, sh);
+    if (rc != SWIFTLLM_OK) return rc;
+    if ((rc = validate_partition(who, partition_size)) != SWIFTLLM_OK) return rc;
+    const int cus = device_cus();
+    const size_t need = v2_bytes(sh, effective_partition(sh, partition_size, cus), cus);
+    if (need > SWIFTLLM_HIP_NOALLOC_SCRATCH_BYTES) {
+        return fail(SWIFTLLM_ERR_INVALID_PARAMETER,
+                    "%s: these sizes need %zu bytes of split-K scratch, more than the %zu bytes of "
+                    "its static scratch; use swiftllm_hip_launch_paged_attention_v2 with a workspace",
+                    who, need, static_cast<size_t>(SWIFTLLM_HIP_NOALLOC_SCRATCH_BYTES));
+    }
+    if ((rc = require_device()) != SWIFTLLM_OK) return rc;
+    if (sh.S == 0) return ok();
+    void* ws = nullptr;
+    if ((rc = static_scratch(&ws, who)) != SWIFTLLM_OK) return rc;
+    return decode_v2(out, ws, SWIFTLLM_HIP_NOALLOC_SCRATCH_BYTES, q, kc, vc, bt, ctx, scale, sh,
+                     partition_size, num_blocks, stream, who);
+}
+
+}  // namespace
+}  // namespace swiftllm
+
 using namespace swiftllm;
 
 extern "C" {
@@ -1241,6 +1324,19 @@ int swiftllm_hip_launch_paged_attention_v2(void* output, void* workspace, size_t
     return decode_v2(output, workspace, workspace_bytes, query, key_cache, value_cache, block_tables,
                      context_lens, scale, sh, partition_size, num_blocks, stream,
                      "swiftllm_hip_launch_paged_attention_v2");
+}
+
+int swiftllm_hip_launch_paged_attention_v2_noalloc(void* output, const void* query,
+                                                   const void* key_cache, const void* value_cache,
+                                                   const int* block_tables, const int* context_lens,
+                                                   float scale, int num_seqs, int num_heads,
+                                                   int num_kv_heads, int head_dim, int block_size,
+                                                   int max_num_blocks_per_seq, int partition_size,
+                                                   int num_blocks, hipStream_t stream) {
+    const Shape sh{num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_num_blocks_per_seq};
+    return decode_v2_noalloc(output, query, key_cache, value_cache, block_tables, context_lens,
+                             scale, sh, partition_size, num_blocks, stream,
+                             "swiftllm_hip_launch_paged_attention_v2_noalloc");
 }
 
 size_t swiftllm_hip_paged_attention_v2_workspace_size(int num_seqs, int num_heads, int num_kv_heads,

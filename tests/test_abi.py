@@ -119,6 +119,23 @@ def test_v2_workspace_size_and_validation():
     assert rc == INVALID  # partition not a multiple of 16
 
 
+def test_v2_noalloc_validation_before_any_device_call():
+    """The no-allocation split-K entry refuses bad shapes and sizes beyond its
+    static scratch on the host, before it looks for a device."""
+    L = _lib.lib()
+    assert _lib.NOALLOC_SCRATCH_BYTES == 64 << 20
+    # 256 x 64 heads x 4096 partitions of 16 tokens x 128 floats: ~34 GB
+    rc = L.swiftllm_hip_launch_paged_attention_v2_noalloc(
+        FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 0.1, 256, 64, 8, 128, 16, 4096, 16, 0, None)
+    assert rc == INVALID and "static scratch" in _lib.last_error()[1]
+    rc = L.swiftllm_hip_launch_paged_attention_v2_noalloc(
+        FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 0.1, 8, 64, 8, 128, 16, 2048, 24, 0, None)
+    assert rc == INVALID  # partition not a multiple of 16
+    rc = L.swiftllm_hip_launch_paged_attention_v2_noalloc(
+        FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 0.1, 8, 64, 8, 96, 16, 2048, 512, 0, None)
+    assert rc == UNSUP  # head_dim 96
+
+
 def test_params_struct_twins_validate():
     p = pa.PagedAttentionParams(2, 32, 8, 96, 16, 0.1, 64)
     with pytest.raises(pa.NotSupported):
