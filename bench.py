@@ -44,14 +44,24 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", type=int, choices=[2, 3, 4, 5, 6, 7, 8, 9], default=2,
-                    help="2: Llama-3-8B decode (the metric's workload); 3: long-context split-K; "
+    ap.add_argument("--config", type=int, choices=[1, 2, 3, 4, 5, 6, 7, 8, 9], default=2,
+                    help="1: tiny MHA decode (BASELINE's CPU-runnable case, us only); "
+                         "2: Llama-3-8B decode (the metric's workload); 3: long-context split-K; "
                          "4: ragged step (cache write + decode); 5: MoE route + dispatch; "
                          "6: copy_blocks (copy-on-write, 32 layers); 7: swap_blocks out and in; "
                          "8: Mixtral MoE MLP (route, dispatch, expert GEMMs, combine); "
                          "9: Llama-3-8B paged prefill (8 prompts of 2048 tokens)")
     ap.add_argument("--variant", choices=["v1", "v2"], default=None,
-                    help="default: v1 for config 2, v2 for configs 3 and 4")
+                    help="default: v1 for configs 1 and 2, v2 for configs 3 and 4")
+    ap.add_argument("--ceiling", choices=["stream", "gather", "store", "rowcopy"], default=None,
+                    help="time one access-pattern ceiling kernel alone (libswiftllm_ceilings) and print "
+                         "its JSON line: the NT read stream; config 2/3/4's tile gather (--load-bytes); "
+                         "config 4's cache-write stores (--store-mode); config 5's row copies")
+    ap.add_argument("--load-bytes", type=int, choices=[8, 16], default=16, help="--ceiling gather")
+    ap.add_argument("--store-mode", type=int, choices=[0, 1, 2], default=1,
+                    help="--ceiling store: 0 four rows per lane, 1 one line per 4 lanes, 2 whole rows")
+    ap.add_argument("--no-ceiling", action="store_true",
+                    help="leave the live ceiling measurement out of the line (for profiles)")
     ap.add_argument("--partition", type=int, default=None,
                     help="v2 partition size in tokens, 0 = balanced (stream-K) scheduling; "
                          "default 4096 for config 3, 1024 for config 4")
@@ -182,6 +192,8 @@ def main():
 
     if args.calib_copy_mib > 0:
         calibrate(args.calib_copy_mib << 20)
+    if args.ceiling:
+        return bench_ceiling(args)
     if args.config == 5:
         return bench_moe(args)
     if args.config in (6, 7):
@@ -193,7 +205,7 @@ def main():
     if args.rotate is None:
         args.rotate = 4
     if args.variant is None:
-        args.variant = "v1" if args.config == 2 else "v2"
+        args.variant = "v1" if args.config in (1, 2) else "v2"
     if args.partition is None:
         # measured defaults: 4096-token partitions for config 3 (long uniform
         # contexts); 1024 for config 4, where the step (cache write + decode)
@@ -307,6 +319,19 @@ def main():
 
     traffic = read_traffic(f"decode_config{args.config}_traffic.json")
 
+    # Ceilings measured in this run, after the timed calls (the store probe
+    # overwrites cache contents): the same K/V tiles read by the gather
+    # kernel alone (and for config 4 the cache write's stores alone), and the
+    # NT sequential read stream.
+    ceiling = stream_gbs = None
+    if not args.no_ceiling:
+        ceiling = decode_ceiling(w, pools, bt, stream, max(args.steps // 4, 20), kv_bytes,
+                                 args.partition if args.variant == "v2" else 0,
+                                 slots if args.config == 4 else None)
+        stream_gbs = measure_stream(stream)[0]
+        print(f"[bench] ceiling {ceiling['value']:.0f} GB/s ({ceiling['us_per_call']:.2f} us), "
+              f"stream {stream_gbs:.0f} GB/s", file=sys.stderr, flush=True)
+
     cpu = None
     if not args.no_cpu:
         import oracle
@@ -321,15 +346,16 @@ def main():
             times.append(time.perf_counter() - t1)
         cpu_s = float(np.median(times))
         cpu = {"value": round(kv_bytes / cpu_s / 1e9, 3), "unit": "GB/s", "cores": int(threads),
-               "kind": "port", "us_per_call": round(cpu_s * 1e6, 1),
+               "kind": "port", "us_per_call": round(cpu_s * 1e6, 1), **host_info(),
                "sample": f"full config-{args.config} batch (same inputs, decode only), fp32 C restatement "
                          f"(oracle/oracle.c, OpenMP over (seq, kv head)), median of {len(times)} runs"}
         print(f"[bench] cpu baseline {cpu_s * 1e3:.1f} ms/call on {threads} threads", file=sys.stderr,
               flush=True)
 
-    workload_name = {2: "llama3-8b-decode-layer", 3: "llama3-70b-long-context-splitk",
+    workload_name = {1: "tiny-mha-decode", 2: "llama3-8b-decode-layer", 3: "llama3-70b-long-context-splitk",
                      4: "ragged-continuous-batching-step"}[args.config]
-    ctx_desc = {2: "uniform[512,4096]", 3: "32768 (all)", 4: "lognormal(median 600, sigma 1) clip [1,8192]"}[args.config]
+    ctx_desc = {1: "uniform[1,256]", 2: "uniform[512,4096]", 3: "32768 (all)",
+                4: "lognormal(median 600, sigma 1) clip [1,8192]"}[args.config]
     rec = {
         "metric": "paged-attn decode KV-read GB/s (% HBM peak) + us/call @ Llama-3-8B shape",
         "value": round(value, 2),
@@ -366,8 +392,20 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
         },
+        "ceiling": ceiling,
+        "ceiling_frac": round(value / ceiling["value"], 4) if ceiling else None,
+        "stream_read_gbs": round(stream_gbs, 2) if stream_gbs else None,
+        "stream_frac": round(value / stream_gbs, 4) if stream_gbs else None,
         "cpu_baseline": cpu,
     }
+    if args.config == 1:
+        # latency-bound (1 MB per call): us/call only, no roofline claim
+        rec["metric"] = "paged-attn decode us/call @ tiny MHA (BASELINE config 1, CPU-runnable case)"
+        rec["value"], rec["unit"], rec["higher_is_better"] = round(ms * 1e3, 3), "us", False
+        rec["roofline"] = None
+        rec["ceiling_frac"] = rec["stream_frac"] = None
+        if cpu:
+            cpu.update(value=cpu["us_per_call"], unit="us")
     if ms512 is not None:
         rec["us_per_call_partition512"] = round(ms512 * 1e3, 3)
         rec["kv_gbs_partition512"] = round(kv_bytes / (ms512 * 1e-3) / 1e9, 2)
@@ -390,6 +428,104 @@ def calibrate(nbytes):
     _hip.synchronize()
     src.free()
     dst.free()
+
+
+def host_info():
+    """Host CPU threads this process may run on and the CPU model, stated
+    beside every CPU baseline."""
+    try:
+        nproc = len(os.sched_getaffinity(0))
+    except AttributeError:
+        nproc = os.cpu_count() or 1
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": nproc, "cpu_model": model}
+
+
+STREAM_BYTES = 2 << 30  # beyond the 256 MB Infinity Cache
+
+
+def measure_stream(stream, steps=20):
+    """The NT sequential read stream of libswiftllm_ceilings over a 2 GiB
+    buffer: (GB/s, us per launch), launches back to back."""
+    from swiftllm_amd import ceilings
+    from swiftllm_amd._hip import DeviceArray
+
+    buf = DeviceArray((STREAM_BYTES // 4,), np.uint32)
+    buf.fill_byte(0x5A)
+    sink = DeviceArray((1,), np.uint32)
+    ms = timed(lambda i: ceilings.read_stream(buf, STREAM_BYTES, sink, stream), stream, steps, 3, 0)[0]
+    buf.free()
+    return STREAM_BYTES / (ms * 1e-3) / 1e9, ms * 1e3
+
+
+def measure_gather(w, pools, bt, stream, steps, load_bytes, partition_tokens):
+    """The decode's K/V tile reads alone (libswiftllm_ceilings tile gather)
+    over the same rotated pools and block tables, in the decode's work items
+    (whole (sequence, kv head) units for the single pass, partitions of
+    partition_tokens for split-K): us per call, launches back to back."""
+    from swiftllm_amd import _hip, ceilings
+    from swiftllm_amd._hip import DeviceArray
+
+    sh = w.shape
+    Hkv = sh["num_kv_heads"]
+    items = ceilings.gather_items(w.context_lens, Hkv, partition_tokens, _hip.cu_count())
+    d_items = DeviceArray.from_numpy(items)
+    sink = DeviceArray((1,), np.uint32)
+
+    def step(i):
+        kc, vc = pools[i % len(pools)]
+        ceilings.tile_gather(kc, vc, bt, d_items, len(items), Hkv, sh["head_dim"],
+                             sh["max_num_blocks_per_seq"], sh["num_blocks"], load_bytes, sink, stream)
+
+    return timed(step, stream, steps, 10, 0)[0] * 1e3
+
+
+def measure_store(w, pools, slots, stream, steps, mode):
+    """reshape_and_cache's stores alone (libswiftllm_ceilings cache store,
+    `mode` as in include/swiftllm_ceilings.h) at the workload's slots, into
+    the same rotated pools: us per call."""
+    from swiftllm_amd import ceilings
+
+    sh = w.shape
+
+    def step(i):
+        kc, vc = pools[i % len(pools)]
+        ceilings.cache_store(kc, vc, slots, sh["num_seqs"], sh["num_kv_heads"], sh["head_dim"],
+                             sh["num_blocks"], mode, stream)
+
+    return timed(step, stream, steps, 10, 0)[0] * 1e3
+
+
+def decode_ceiling(w, pools, bt, stream, steps, kv_bytes, partition_tokens, slots=None):
+    """The access-pattern ceiling of a decode call: the tile gather at 8- and
+    16-byte loads in the decode's own work items (the faster counts), plus
+    for a ragged step the cache write's stores (modes 0 and 1, the faster
+    counts). Returns the ceiling record; its value is K/V bytes / the
+    pattern's time, like `value`. Run it after the timed calls: the store
+    probe overwrites cache contents."""
+    g8 = measure_gather(w, pools, bt, stream, steps, 8, partition_tokens)
+    g16 = measure_gather(w, pools, bt, stream, steps, 16, partition_tokens)
+    rec = {"pattern": "tile gather of the call's K/V tiles in its work items (libswiftllm_ceilings, "
+                      "NT loads)", "partition_tokens": partition_tokens,
+           "gather8_us": round(g8, 3), "gather16_us": round(g16, 3)}
+    t = min(g8, g16)
+    if slots is not None:
+        st = [measure_store(w, pools, slots, stream, steps, m) for m in (0, 1, 2)]
+        rec["pattern"] += " + reshape_and_cache's 2-byte stores"
+        rec["store_us_4rows_per_lane"] = round(st[0], 3)
+        rec["store_us_line_per_4_lanes"] = round(st[1], 3)
+        rec["store_us_whole_rows"] = round(st[2], 3)
+        t += min(st[0], st[1])
+    rec.update(value=round(kv_bytes / (t * 1e-6) / 1e9, 2), unit="GB/s", us_per_call=round(t, 3))
+    return rec
 
 
 def read_traffic(name):
@@ -431,6 +567,71 @@ def timed(step, stream, steps, warmup, samples):
     return (ms,) + tuple(float(np.percentile(per, x)) for x in (10, 50, 90))
 
 
+def bench_ceiling(args):
+    """`--ceiling`: one access-pattern kernel of libswiftllm_ceilings timed
+    alone, for its rocprofv3 profile and as the committed source of the
+    ceilings the other lines measure live. Prints one JSON line (GB/s of the
+    pattern's own bytes)."""
+    from swiftllm_amd import ceilings, workloads
+    from swiftllm_amd._hip import DeviceArray, Stream
+
+    stream = Stream()
+    steps = max(args.steps // 4, 20)
+    if args.ceiling == "stream":
+        gbs, us = measure_stream(stream, steps)
+        nbytes, work = STREAM_BYTES, {"workload": "nt-read-stream", "bytes_per_call": STREAM_BYTES,
+                                      "loads": "16-byte nontemporal, grid-stride"}
+    elif args.ceiling in ("gather", "store"):
+        cfg = args.config if args.config in (2, 3, 4) else (4 if args.ceiling == "store" else 2)
+        w = workloads.decode_config(cfg, seed=args.seed)
+        sh = w.shape
+        pools = [(DeviceArray.from_numpy(w.key_cache), DeviceArray.from_numpy(w.value_cache))
+                 for _ in range(max(1, args.rotate or 4))]
+        bt, ctx = DeviceArray.from_numpy(w.block_tables), DeviceArray.from_numpy(w.context_lens)
+        if args.ceiling == "gather":
+            part = args.partition if args.partition is not None else {2: 0, 3: 4096, 4: 1024}[cfg]
+            us = measure_gather(w, pools, bt, stream, steps, args.load_bytes, part)
+            nbytes = w.kv_bytes()
+            work = {"workload": f"config{cfg}-tile-gather", "load_bytes": args.load_bytes,
+                    "partition_tokens": part, "kv_bytes_per_call": nbytes,
+                    "kv_pool_copies_rotated": len(pools)}
+        else:
+            if w.slot_mapping is None:
+                raise SystemExit("--ceiling store needs config 4 (a ragged step with new tokens)")
+            slots = DeviceArray.from_numpy(w.slot_mapping)
+            us = measure_store(w, pools, slots, stream, steps, args.store_mode)
+            nbytes = 2 * sh["num_seqs"] * sh["num_kv_heads"] * sh["head_dim"] * 2
+            work = {"workload": f"config{cfg}-cache-write-stores", "store_mode": args.store_mode,
+                    "tokens": sh["num_seqs"], "bytes_written_per_call": nbytes,
+                    "kv_pool_copies_rotated": len(pools)}
+        gbs = nbytes / (us * 1e-6) / 1e9
+    else:
+        wl = workloads.moe_config(seed=args.seed)
+        T, hidden = wl.x.shape
+        K = wl.top_k
+        copies = max(1, args.rotate or 8)
+        rng = np.random.default_rng(args.seed)
+        rows = [DeviceArray.from_numpy(rng.permutation(T * K).astype(np.int32).reshape(T, K))
+                for _ in range(copies)]
+        xs = [DeviceArray.from_numpy(wl.x) for _ in range(copies)]
+        dst = [DeviceArray((T * K, hidden), np.float16) for _ in range(copies)]
+
+        def step(i):
+            c = i % copies
+            ceilings.row_copy(xs[c], dst[c], rows[c], T, K, hidden, T * K, stream)
+
+        us = timed(step, stream, steps, 10, 0)[0] * 1e3
+        nbytes = 2 * T * hidden + 2 * T * K * hidden
+        gbs = nbytes / (us * 1e-6) / 1e9
+        work = {"workload": "config5-row-copy", "tokens": T, "hidden": hidden, "top_k": K,
+                "bytes_per_call": nbytes, "copies_rotated": copies}
+    rec = {"metric": f"{args.ceiling} ceiling GB/s (libswiftllm_ceilings)", "value": round(gbs, 2),
+           "unit": "GB/s", "n_gpus": 1, "us_per_call": round(us, 3),
+           "hbm_peak_frac": round(gbs / HBM_PEAK_GBS, 4), "higher_is_better": True,
+           "dtype": "u8 (memory access pattern only)", "data": "synthetic", "config": work}
+    print(json.dumps(rec), flush=True)
+
+
 def bench_moe(args):
     """Config 5: Mixtral-8x7B-style routing + dispatch (4096 tokens, hidden 4096,
     8 experts, top-2). Eight copies of the activations and outputs rotate so
@@ -462,21 +663,42 @@ def bench_moe(args):
     ms, p10, p50, p90 = timed(step, stream, args.steps, args.warmup, args.samples)
     alg = wl.bytes()
     value = alg / (ms * 1e-3) / 1e9
+
+    # Ceiling measured in this run: the call's row copies alone (each row read
+    # once, written to its top-k destinations at the rows the dispatch chose),
+    # over the same rotated buffers; and the NT sequential read stream.
+    ceiling = stream_gbs = None
+    if not args.no_ceiling:
+        from swiftllm_amd import ceilings
+
+        rows = [b.inverse for b in bufs]
+
+        def copy_step(i):
+            c = i % copies
+            ceilings.row_copy(xs[c], bufs[c].x_perm, rows[c], T, K, hidden, T * K, stream)
+
+        t_copy = timed(copy_step, stream, max(args.steps // 4, 20), 10, 0)[0] * 1e3
+        ceiling = {"pattern": "the call's row copies alone (libswiftllm_ceilings row copy, 16-byte "
+                              "NT loads and stores, destinations from the dispatch)",
+                   "value": round(alg / (t_copy * 1e-6) / 1e9, 2), "unit": "GB/s",
+                   "us_per_call": round(t_copy, 3)}
+        stream_gbs = measure_stream(stream)[0]
     cpu = None
     if not args.no_cpu:
         import oracle
 
+        oracle.moe_route_dispatch_serial(wl.logits, wl.x, K)
         t_budget, times = time.time(), []
         while len(times) < 5 and time.time() - t_budget < 20.0:
             t1 = time.perf_counter()
-            rids, _ = oracle.moe_route(wl.logits, K)
-            _, _, _, sorted_ids = oracle.moe_dispatch(rids, E)
-            _ = wl.x[sorted_ids]
+            oracle.moe_route_dispatch_serial(wl.logits, wl.x, K)
             times.append(time.perf_counter() - t1)
         cpu_s = float(np.median(times))
         cpu = {"value": round(alg / cpu_s / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-               "us_per_call": round(cpu_s * 1e6, 1),
-               "sample": "full config-5 batch: numpy/Python oracle route + stable counting sort + row gather"}
+               "us_per_call": round(cpu_s * 1e6, 1), **host_info(),
+               "sample": f"full config-5 batch: C restatement on one thread (oracle/oracle.c "
+                         f"oracle_moe_route_dispatch_serial: fp32 softmax, top-2, serial counting "
+                         f"sort, row copies), median of {len(times)} runs"}
     rec = {
         "metric": "MoE top-2 route + dispatch GB/s (algorithmic bytes) + us/call @ Mixtral-8x7B shape",
         "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -493,6 +715,10 @@ def bench_moe(args):
         "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(value / HBM_PEAK_GBS, 4),
                      "traffic": read_traffic("moe_config5_traffic.json")},
+        "ceiling": ceiling,
+        "ceiling_frac": round(value / ceiling["value"], 4) if ceiling else None,
+        "stream_read_gbs": round(stream_gbs, 2) if stream_gbs else None,
+        "stream_frac": round(value / stream_gbs, 4) if stream_gbs else None,
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)

@@ -20,6 +20,9 @@ reference repository; "cu:" = crates/swiftllm-cuda/kernels/paged_attention.cu):
   moe_route / moe_dispatch   mlp.rs:240-246 steps with sampling/mod.rs:366-385
                              conventions (max-subtracted softmax, stable
                              descending order)
+  moe_route_dispatch_serial  C, one thread: the same route (fp32 softmax) and a
+                             serial counting sort with the row copies (the MoE
+                             CPU baseline)
   copy_blocks / swap_blocks  numpy: cu:201-227 (launcher cu:302-327) and
                              crates/swiftllm-cuda/src/bindings.rs:200-242
   silu / moe_expert_gemm /   numpy: MoeMlp steps 3-4 (mlp.rs:240-246) over
@@ -65,6 +68,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_reshape_and_cache.argtypes = [vp, vp, vp, vp, vp, i, i, i, i]
         L.oracle_reshape_and_cache.restype = None
         L.oracle_max_threads.restype = i
+        L.oracle_moe_route_dispatch_serial.argtypes = [vp, vp, i, i, i, i] + [vp] * 7
+        L.oracle_moe_route_dispatch_serial.restype = None
         L.oracle_set_threads.argtypes = [i]
         _LIB = L
     return _LIB
@@ -306,3 +311,26 @@ def moe_dispatch(ids: np.ndarray, num_experts: int):
             inverse[idx] = row
             sorted_ids[row] = idx // K
     return counts, offsets, inverse.reshape(T, K), sorted_ids
+
+
+def moe_route_dispatch_serial(logits: np.ndarray, x: np.ndarray, top_k: int):
+    """C restatement (one thread) of moe_route + moe_dispatch + the row copy:
+    fp32 softmax, k argmax passes with ties to the lower index, a serial
+    counting sort. Returns (ids, weights fp32, counts, offsets, x_perm,
+    inverse, sorted_token_ids)."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    xs = _u16(x)
+    T, E = lg.shape
+    hidden = xs.shape[1]
+    ids = np.empty((T, top_k), np.int32)
+    w = np.empty((T, top_k), np.float32)
+    counts = np.empty(E, np.int32)
+    offsets = np.empty(E + 1, np.int32)
+    x_perm = np.empty((T * top_k, hidden), np.uint16)
+    inverse = np.empty((T, top_k), np.int32)
+    sorted_ids = np.empty(T * top_k, np.int32)
+    lib().oracle_moe_route_dispatch_serial(lg.ctypes.data, xs.ctypes.data, T, E, top_k, hidden,
+                                           ids.ctypes.data, w.ctypes.data, counts.ctypes.data,
+                                           offsets.ctypes.data, x_perm.ctypes.data,
+                                           inverse.ctypes.data, sorted_ids.ctypes.data)
+    return ids, w, counts, offsets, x_perm.view(np.float16), inverse, sorted_ids

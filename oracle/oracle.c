@@ -243,3 +243,60 @@ void oracle_reshape_and_cache(const uint16_t* key, const uint16_t* value, uint16
         }
     }
 }
+
+/*
+ * MoE routing and dispatch on one thread: the CPU baseline of the MoE row
+ * (MoeMlp::forward steps 1-2, crates/swiftllm-models/src/layers/mlp.rs:
+ * 240-246, whose reference body returns zeros) with the sampling
+ * conventions of crates/swiftllm-core/src/sampling/mod.rs:366-385:
+ *   - fp32 softmax with the row max subtracted (:380-385);
+ *   - top-k by k argmax passes over the logits, ties to the lower expert
+ *     index (the stable descending sort of :367-377), weights = the selected
+ *     probabilities renormalised to sum 1;
+ *   - a serial counting sort of the (t, k) entries by expert: histogram,
+ *     exclusive prefix, then placement in (t asc, k asc) order, which is
+ *     stable; x_perm[row] = x[t] (row copy), inverse[t, k] = row,
+ *     sorted_token_ids[row] = t.
+ * K <= 8 and E <= 256, as the device path accepts.
+ */
+void oracle_moe_route_dispatch_serial(const float* logits, const uint16_t* x, int T, int E, int K,
+                                      int hidden, int32_t* ids, float* weights, int32_t* counts,
+                                      int32_t* offsets, uint16_t* x_perm, int32_t* inverse,
+                                      int32_t* sorted_token_ids) {
+    for (int t = 0; t < T; ++t) {
+        const float* row = logits + (size_t)t * E;
+        float mx = row[0];
+        for (int e = 1; e < E; ++e) mx = row[e] > mx ? row[e] : mx;
+        float sum = 0.0f;
+        for (int e = 0; e < E; ++e) sum += expf(row[e] - mx);
+        unsigned char taken[256] = {0};
+        float psel[8];
+        float psum = 0.0f;
+        for (int k = 0; k < K; ++k) {
+            int best = -1;
+            for (int e = 0; e < E; ++e) {
+                if (!taken[e] && (best < 0 || row[e] > row[best])) best = e;
+            }
+            taken[best] = 1;
+            ids[(size_t)t * K + k] = best;
+            psel[k] = expf(row[best] - mx) / sum;
+            psum += psel[k];
+        }
+        for (int k = 0; k < K; ++k) weights[(size_t)t * K + k] = psel[k] / psum;
+    }
+    for (int e = 0; e < E; ++e) counts[e] = 0;
+    for (size_t i = 0; i < (size_t)T * K; ++i) counts[ids[i]] += 1;
+    offsets[0] = 0;
+    for (int e = 0; e < E; ++e) offsets[e + 1] = offsets[e] + counts[e];
+    int32_t fill[256];
+    for (int e = 0; e < E; ++e) fill[e] = offsets[e];
+    for (int t = 0; t < T; ++t) {
+        for (int k = 0; k < K; ++k) {
+            const int e = ids[(size_t)t * K + k];
+            const int r = fill[e]++;
+            inverse[(size_t)t * K + k] = r;
+            sorted_token_ids[r] = t;
+            memcpy(x_perm + (size_t)r * hidden, x + (size_t)t * hidden, sizeof(uint16_t) * hidden);
+        }
+    }
+}

@@ -3,8 +3,9 @@
     python -m swiftllm_amd.build          # or swiftllm_amd.build.build()
 
 Every HIP source under csrc/ is compiled to an object in csrc/_build/ and
-linked into swiftllm_amd/libswiftllm_hip.so next to this file, so the
-library travels with the source tree.
+linked into swiftllm_amd/libswiftllm_hip.so (the path) or
+swiftllm_amd/libswiftllm_ceilings.so (measurement kernels) next to this file,
+so the libraries travel with the source tree.
 """
 
 from __future__ import annotations
@@ -24,6 +25,11 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
 SOURCES = ["abi.cpp", "paged_attention.hip", "prefill.hip", "cache_ops.hip", "block_copy.hip", "moe.hip", "moe_experts.hip"]
+
+# The measurement kernels bench.py times beside the path (include/swiftllm_ceilings.h)
+# are a library of their own, outside the drop-in interface.
+CEILINGS_LIB = PKG / "libswiftllm_ceilings.so"
+CEILINGS_SOURCES = ["ceilings.hip"]
 
 FLAGS = [
     "-O3",
@@ -51,11 +57,25 @@ def _run(cmd: list[str]) -> None:
         print(out, file=sys.stderr)
 
 
+def _link(lib: Path, sources: list[str], verbose: bool) -> None:
+    tmp = lib.with_suffix(".so.tmp")
+    link = [
+        HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}",
+        *[str(OBJ / (s + ".o")) for s in sources],
+        "-Wl,-rpath,/opt/rocm/lib", "-o", str(tmp),
+    ]
+    if verbose:
+        print(" ".join(link))
+    _run(link)
+    os.replace(tmp, lib)
+
+
 def build(verbose: bool = False) -> Path:
-    """Compile every source and link the shared library; returns its path."""
+    """Compile every source and link both shared libraries; returns the path
+    of libswiftllm_hip.so."""
     OBJ.mkdir(parents=True, exist_ok=True)
     jobs = []
-    for src in SOURCES:
+    for src in SOURCES + CEILINGS_SOURCES:
         obj = OBJ / (src + ".o")
         lang = ["-x", "hip"]
         jobs.append([HIPCC, *FLAGS, *lang, "-c", str(CSRC / src), "-o", str(obj)])
@@ -64,16 +84,8 @@ def build(verbose: bool = False) -> Path:
             if verbose:
                 print(" ".join(cmd))
         list(ex.map(_run, jobs))
-    tmp = LIB.with_suffix(".so.tmp")
-    link = [
-        HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}",
-        *[str(OBJ / (s + ".o")) for s in SOURCES],
-        "-Wl,-rpath,/opt/rocm/lib", "-o", str(tmp),
-    ]
-    if verbose:
-        print(" ".join(link))
-    _run(link)
-    os.replace(tmp, LIB)
+    _link(LIB, SOURCES, verbose)
+    _link(CEILINGS_LIB, CEILINGS_SOURCES, verbose)
     return LIB
 
 

@@ -10,11 +10,14 @@
 // slots are skipped (padding tokens), and slots past num_blocks * BS are
 // skipped when the pool size is known.
 //
-// One workgroup per token. Reads of the token's Hkv*D row are contiguous;
-// each element lands in a different 2-byte column of the [D][BS] tile, which
-// is the layout's price for having contiguous tokens on the decode side.
-// At decode sizes the kernel is bound by those partial-row writes (config 4:
-// 2 x 256 x 8 x 128 of them in ~21 us), not by bytes.
+// One workgroup per token, consecutive lanes on consecutive rows. Row
+// r = h * D + d of block b is the 16 tokens of (h, d) at element
+// (b * Hkv * D + r) * BS; the token's element goes to column o of it. Four
+// rows make a 128-byte line (BS 16), so one wave store instruction covers 16
+// whole lines with 8 bytes each, where a lane per 4 consecutive d (four
+// stores to the 4 rows of one line) needs 64 lines per instruction and four
+// instructions per line. Measured alone on MI355X (the stores of config 4's
+// 256 tokens, no loads): 8.7 us against 23.4 us.
 
 #include "common.hpp"
 
@@ -46,11 +49,10 @@ __device__ __forceinline__ void put(uint16_t* p, uint16_t v) {
     __builtin_nontemporal_store(v, p);
 }
 
-// VEC: each thread moves 4 consecutive elements of one head (one 8-byte load
-// of key and of value; needs D % 4 == 0 and 8-byte aligned rows), so at
-// Llama-3-8B's 1024 elements per token every load of a workgroup is issued
-// at once.
-template <bool VEC>
+// Rows per thread per pass: a pass of 256 threads covers 1024 rows, all of
+// Llama-3-8B's Hkv * D; its 8 loads per thread are issued before any store.
+constexpr int kRowsPerThread = 4;
+
 __global__ __launch_bounds__(256) void reshape_and_cache_kernel(const CacheArgs a) {
     const int t = blockIdx.x;
     const int slot = a.slots[t];
@@ -60,31 +62,25 @@ __global__ __launch_bounds__(256) void reshape_and_cache_kernel(const CacheArgs 
     const int n = a.Hkv * a.D;
     const uint16_t* kr = a.key + t * a.key_stride;
     const uint16_t* vr = a.value + t * a.value_stride;
-    const size_t tile = static_cast<size_t>(a.D) * a.BS;
-    const size_t blk = static_cast<size_t>(b) * a.Hkv * tile + o;
-    if constexpr (VEC) {
-        for (int e = threadIdx.x * 4; e < n; e += blockDim.x * 4) {
-            const uint2 kw = *reinterpret_cast<const uint2*>(kr + e);
-            const uint2 vw = *reinterpret_cast<const uint2*>(vr + e);
-            const int h = e / a.D;
-            const int d = e - h * a.D;
-            const size_t dst = blk + h * tile + static_cast<size_t>(d) * a.BS;
-            put(a.kc + dst, static_cast<uint16_t>(kw.x));
-            put(a.kc + dst + a.BS, static_cast<uint16_t>(kw.x >> 16));
-            put(a.kc + dst + 2 * a.BS, static_cast<uint16_t>(kw.y));
-            put(a.kc + dst + 3 * a.BS, static_cast<uint16_t>(kw.y >> 16));
-            put(a.vc + dst, static_cast<uint16_t>(vw.x));
-            put(a.vc + dst + a.BS, static_cast<uint16_t>(vw.x >> 16));
-            put(a.vc + dst + 2 * a.BS, static_cast<uint16_t>(vw.y));
-            put(a.vc + dst + 3 * a.BS, static_cast<uint16_t>(vw.y >> 16));
+    uint16_t* kdst = a.kc + static_cast<size_t>(b) * n * a.BS + o;
+    uint16_t* vdst = a.vc + static_cast<size_t>(b) * n * a.BS + o;
+    for (int r0 = 0; r0 < n; r0 += 256 * kRowsPerThread) {
+        uint16_t kv[kRowsPerThread], vv[kRowsPerThread];
+#pragma unroll
+        for (int i = 0; i < kRowsPerThread; ++i) {
+            const int r = r0 + i * 256 + threadIdx.x;
+            if (r < n) {
+                kv[i] = kr[r];
+                vv[i] = vr[r];
+            }
         }
-    } else {
-        for (int e = threadIdx.x; e < n; e += blockDim.x) {
-            const int h = e / a.D;
-            const int d = e - h * a.D;
-            const size_t dst = blk + h * tile + static_cast<size_t>(d) * a.BS;
-            put(a.kc + dst, kr[e]);
-            put(a.vc + dst, vr[e]);
+#pragma unroll
+        for (int i = 0; i < kRowsPerThread; ++i) {
+            const int r = r0 + i * 256 + threadIdx.x;
+            if (r < n) {
+                put(kdst + static_cast<size_t>(r) * a.BS, kv[i]);
+                put(vdst + static_cast<size_t>(r) * a.BS, vv[i]);
+            }
         }
     }
 }
@@ -119,9 +115,7 @@ int reshape_and_cache(const void* key, const void* value, void* key_cache, void*
     a.Hkv = num_kv_heads;
     a.D = head_dim;
     a.BS = block_size;
-    const bool vec = head_dim % 4 == 0 && aligned(key, 8) && aligned(value, 8);
-    return launched(launch(vec ? reshape_and_cache_kernel<true> : reshape_and_cache_kernel<false>,
-                           dim3(num_tokens), dim3(256), 0, stream, a),
+    return launched(launch(reshape_and_cache_kernel, dim3(num_tokens), dim3(256), 0, stream, a),
                     who);
 }
 

@@ -301,16 +301,29 @@ void paged_decode_kernel(const DecodeArgs a) {
 }
 
 // Split-K partitions. The items are the real (sequence, partition) pairs
-// times the kv-head chunks: every workgroup builds the prefix of partitions
-// per sequence in LDS and walks items blockIdx.x, + gridDim.x, ... The grid
-// is sized to the resident workgroups, not to the worst case of every
-// sequence, so a ragged batch launches no empty workgroups (a grid over
-// max_num_blocks_per_seq would be mostly empty). Batches of more than
-// kPartMaxSeqs sequences take one item per workgroup over the full grid.
+// times the kv-head chunks, longest first: every workgroup lists them in LDS
+// and walks items blockIdx.x, + gridDim.x, ... The grid is sized to the
+// resident workgroups, not to the worst case of every sequence, so a ragged
+// batch launches no empty workgroups (a grid over max_num_blocks_per_seq
+// would be mostly empty). Workgroups start in blockIdx order, so the order of
+// the list is the order the items start in: first every full partition
+// (part_blocks blocks), then the last, partial partition of each sequence in
+// kLptClasses length classes, longest first (an empty sequence's item, which
+// writes zeros, is a partial of length 0). Measured with the gather kernel
+// of libswiftllm_ceilings on config 4's items at 1024-token partitions:
+// 151 us longest first against 166 us in sequence order.
+//
+// The item of one list position is run by several workgroups (one per kv-head
+// chunk), each with its own copy of the list, so the list must come out the
+// same in every workgroup: within a class the partials keep sequence order,
+// placed by prefix sums, never by the order atomics happen to land in.
+// Batches of more than kPartMaxSeqs sequences take one item per workgroup
+// over the full grid.
 constexpr int kPartMaxSeqs = 4096;
+constexpr int kLptClasses = 16;  // counted in 16-bit fields, two per int
 
 template <int D, int NW>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
 void paged_partition_kernel(const DecodeArgs a) {
     const int HC = a.Hkv * a.nhc;
     if (a.S > kPartMaxSeqs) {
@@ -321,20 +334,52 @@ void paged_partition_kernel(const DecodeArgs a) {
         if (s < a.S) decode_item<D, NW>(a, s, sub / a.nhc, sub % a.nhc, part);
         return;
     }
-    __shared__ int s_pre[kPartMaxSeqs + 1];
+    constexpr int kPacked = kLptClasses / 2;
+    __shared__ int s_pre[kPartMaxSeqs + 1];          // exclusive prefix of full partitions
+    __shared__ unsigned short s_part[kPartMaxSeqs];  // sequences with a partial, longest first
+    __shared__ int s_wpk[NW][kPacked];               // per-wave class counts of a chunk
+    __shared__ int s_cls[kLptClasses];               // next list position of each class
     __shared__ int s_wave[NW];
     const int lane = threadIdx.x & 63;
     const int w = threadIdx.x >> 6;
-    // Partitions per sequence (at least one: an empty sequence's item
-    // writes its zeros), exclusive prefix in chunks of the workgroup.
+    const int pb = a.part_blocks;
+    auto nblk_of = [&](int sq) {
+        const int L = max(a.ctx[sq], 0);
+        return min((L + kBlockTokens - 1) / kBlockTokens, a.MB);
+    };
+    // Class of a sequence's partial partition (0 = longest), or -1 when its
+    // last partition is full.
+    auto class_of = [&](int nblk) {
+        const int rem = nblk - (nblk / pb) * pb;
+        if (rem == 0 && nblk > 0) return -1;
+        return kLptClasses - 1 - static_cast<int>((static_cast<long long>(rem) * kLptClasses) / pb);
+    };
+    // Inclusive scan over the wave of 8 packed ints (two 16-bit class counts
+    // each; a workgroup chunk holds at most 256 of any class).
+    auto wave_scan8 = [&](int (&x)[kPacked]) {
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+#pragma unroll
+            for (int i = 0; i < kPacked; ++i) {
+                const int y = __shfl_up(x[i], d);
+                if (lane >= d) x[i] += y;
+            }
+        }
+    };
+    auto field = [](const int (&x)[kPacked], int c) { return (x[c >> 1] >> (16 * (c & 1))) & 0xffff; };
+    // Pass 1: full partitions per sequence (exclusive prefix, in chunks of
+    // the workgroup) and partials per class.
     int carry = 0;
+    int cls_total[kPacked] = {};
     for (int c0 = 0; c0 < a.S; c0 += NW * 64) {
         const int sq = c0 + static_cast<int>(threadIdx.x);
         int v = 0;
+        int pk[kPacked] = {};
         if (sq < a.S) {
-            const int L = max(a.ctx[sq], 0);
-            const int nblk = min((L + kBlockTokens - 1) / kBlockTokens, a.MB);
-            v = max((nblk + a.part_blocks - 1) / a.part_blocks, 1);
+            const int nblk = nblk_of(sq);
+            v = nblk / pb;
+            const int c = class_of(nblk);
+            if (c >= 0) pk[c >> 1] = 1 << (16 * (c & 1));
         }
         int x = v;
 #pragma unroll
@@ -342,29 +387,89 @@ void paged_partition_kernel(const DecodeArgs a) {
             const int y = __shfl_up(x, d);
             if (lane >= d) x += y;
         }
-        if (lane == 63) s_wave[w] = x;
+        wave_scan8(pk);
+        if (lane == 63) {
+            s_wave[w] = x;
+#pragma unroll
+            for (int i = 0; i < kPacked; ++i) s_wpk[w][i] = pk[i];
+        }
         __syncthreads();
         int before = carry, chunk = 0;
         for (int i = 0; i < NW; ++i) {
             before += (i < w) ? s_wave[i] : 0;
             chunk += s_wave[i];
+#pragma unroll
+            for (int j = 0; j < kPacked; ++j) cls_total[j] += s_wpk[i][j];
         }
         if (sq < a.S) s_pre[sq] = before + x - v;
         carry += chunk;
         __syncthreads();
     }
-    if (threadIdx.x == 0) s_pre[a.S] = carry;
+    // First list position of each class (every thread holds the totals).
+    if (threadIdx.x == 0) {
+        int pos = 0;
+        for (int c = 0; c < kLptClasses; ++c) {
+            s_cls[c] = pos;
+            pos += field(cls_total, c);
+        }
+        s_pre[a.S] = carry;
+    }
+    int npartial = 0;
+#pragma unroll
+    for (int c = 0; c < kLptClasses; ++c) npartial += field(cls_total, c);
     __syncthreads();
-    const int total = carry * HC;
+    // Pass 2: each partial at its class's next position, in sequence order:
+    // the position is the class cursor plus the number of lower-numbered
+    // sequences of the same class in this chunk.
+    for (int c0 = 0; c0 < a.S; c0 += NW * 64) {
+        const int sq = c0 + static_cast<int>(threadIdx.x);
+        int c = -1;
+        int pk[kPacked] = {};
+        if (sq < a.S) {
+            c = class_of(nblk_of(sq));
+            if (c >= 0) pk[c >> 1] = 1 << (16 * (c & 1));
+        }
+        int incl[kPacked];
+#pragma unroll
+        for (int i = 0; i < kPacked; ++i) incl[i] = pk[i];
+        wave_scan8(incl);
+        if (lane == 63) {
+#pragma unroll
+            for (int i = 0; i < kPacked; ++i) s_wpk[w][i] = incl[i];
+        }
+        __syncthreads();
+        if (c >= 0) {
+            int rank = field(incl, c) - 1;
+            for (int i = 0; i < w; ++i) rank += (s_wpk[i][c >> 1] >> (16 * (c & 1))) & 0xffff;
+            s_part[s_cls[c] + rank] = static_cast<unsigned short>(sq);
+        }
+        __syncthreads();
+        if (threadIdx.x < kLptClasses) {
+            int n = 0;
+            for (int i = 0; i < NW; ++i) n += (s_wpk[i][threadIdx.x >> 1] >> (16 * (threadIdx.x & 1))) & 0xffff;
+            s_cls[threadIdx.x] += n;
+        }
+        __syncthreads();
+    }
+    const int nfull = carry;
+    const int total = (nfull + npartial) * HC;
     for (int it = blockIdx.x; it < total; it += gridDim.x) {
         const int pidx = it / HC;
         const int sub = it - pidx * HC;
-        int lo = 0, hi = a.S;  // s_pre[lo] <= pidx < s_pre[hi]
-        while (hi - lo > 1) {
-            const int mid = (lo + hi) >> 1;
-            if (s_pre[mid] <= pidx) lo = mid; else hi = mid;
+        int sq, part;
+        if (pidx < nfull) {
+            int lo = 0, hi = a.S;  // s_pre[lo] <= pidx < s_pre[hi]
+            while (hi - lo > 1) {
+                const int mid = (lo + hi) >> 1;
+                if (s_pre[mid] <= pidx) lo = mid; else hi = mid;
+            }
+            sq = lo;
+            part = pidx - s_pre[lo];
+        } else {
+            sq = s_part[pidx - nfull];
+            part = s_pre[sq + 1] - s_pre[sq];  // after the full ones
         }
-        decode_item<D, NW>(a, lo, sub / a.nhc, sub % a.nhc, pidx - s_pre[lo]);
+        decode_item<D, NW>(a, sq, sub / a.nhc, sub % a.nhc, part);
         __syncthreads();  // the item's LDS is free again
     }
 }

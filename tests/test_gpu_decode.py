@@ -366,3 +366,23 @@ def test_more_sequences_than_the_lds_tables(dev):
         out = dw.run(variant, partition_size=ps)
         assert np.all(out[~live] == 0), f"{variant} ps={ps}: empty sequences must be zero"
         assert_attention_close(out[live], ref[live], f"4500 seqs {variant} ps={ps}")
+
+
+@pytest.mark.parametrize("S,ps", [(300, 64), (1100, 32), (4096, 16)])
+def test_partition_items_longest_first_cover_every_partition(dev, S, ps):
+    """The split-K kernel orders its items longest first in a list that every
+    workgroup builds in its own LDS; the items of one list position are run
+    by different workgroups (one per kv head), so the list must come out the
+    same in each. Ragged batches of more than one 256-sequence chunk, at
+    partitions small enough that every workgroup walks many items and every
+    length class holds ties, with empty sequences: every partition of every
+    sequence is attended exactly once (a missing one leaves the output
+    unwritten or the reduce short of a fragment)."""
+    rng = np.random.default_rng(S + ps)
+    lens = np.clip(np.rint(np.exp(rng.normal(np.log(90.0), 1.0, size=S))), 0, 1500).astype(np.int64)
+    lens[rng.choice(S, size=S // 10, replace=False)] = 0
+    w = _random_batch(rng, lens, H=8, Hkv=2, D=64)
+    out = DeviceWorkload(w).run("v2", partition_size=ps)
+    live = lens > 0
+    assert np.all(out[~live] == 0), "empty sequences must be zero"
+    assert_attention_close(out[live], _ref(w)[live], f"{S} ragged seqs ps={ps}")

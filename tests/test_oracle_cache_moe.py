@@ -161,6 +161,42 @@ def test_dispatch_matches_brute_force(T, E, K):
             assert offsets[ids[t, k]] <= r < offsets[ids[t, k] + 1]
 
 
+@pytest.mark.parametrize("T,E,K,hidden", [(64, 8, 2, 64), (37, 16, 4, 8), (9, 5, 5, 16),
+                                          (130, 64, 8, 24)])
+def test_serial_route_dispatch_matches_brute_force(T, E, K, hidden):
+    """The one-thread C route + counting sort (the MoE CPU baseline) against
+    the brute-force sort of the logits and the brute-force collection of
+    entries per expert: ids, counts, offsets, inverse, sorted ids and the
+    permuted rows bit-exact, fp32 weights within 1e-6 of fp64."""
+    rng = np.random.default_rng(T + E + K)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    logits[0, :3] = logits[0, E - 1]                           # ties
+    logits[1, :] = 0.0                                         # all tied
+    x = rng.standard_normal((T, hidden)).astype(np.float16)
+    ids, w, counts, offsets, x_perm, inverse, sorted_ids = oracle.moe_route_dispatch_serial(logits, x, K)
+    bids, bw = _route_brute(logits, K)
+    assert np.array_equal(ids, bids)
+    assert np.abs(w - bw).max() < 1e-6
+    bc, binv, bsorted = _dispatch_brute(bids, E)
+    assert np.array_equal(counts, bc)
+    assert np.array_equal(offsets, np.concatenate([[0], np.cumsum(bc)]))
+    assert np.array_equal(inverse, binv)
+    assert np.array_equal(sorted_ids, bsorted)
+    assert np.array_equal(x_perm.view(np.uint16), x[bsorted].view(np.uint16))
+
+
+def test_planted_unstable_placement_is_caught():
+    """Placing entries in (k, t) order instead of (t, k) changes the rows."""
+    ids = np.array([[0, 1], [1, 0], [0, 1]], np.int32)
+    _, binv, _ = _dispatch_brute(ids, 2)
+    rows, fill = np.empty_like(binv), [0, 3]
+    for k in range(2):
+        for t in range(3):
+            rows[t, k] = fill[ids[t, k]]
+            fill[ids[t, k]] += 1
+    assert not np.array_equal(rows, binv)
+
+
 def test_dispatch_drops_out_of_range_ids():
     ids = np.array([[0, -1], [5, 1], [1, 0]], np.int32)
     counts, offsets, inverse, sorted_ids = oracle.moe_dispatch(ids, 4)
