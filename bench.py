@@ -1,8 +1,9 @@
 #!/usr/bin/env python3
 """Benchmark of the paged-attention decode hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2|3|4|5]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1..9]
                     [--variant v2|v1] [--partition P] [--rotate R] [--no-cpu]
+                    [--no-ceiling] [--ceiling stream|gather|store|rowcopy]
 
 Workload: Llama-3-8B layer decode (32 query heads, 8 kv heads, head_dim 128,
 block_size 16, batch 64, context lengths uniform in [512, 4096], randomly
@@ -13,13 +14,19 @@ rotated between calls so no call finds its 604 MB of K/V in the 256 MB
 Infinity Cache.
 
 Prints one JSON line: the metric (KV-read GB/s), us/call, the roofline of the
-decode kernel (algorithmic bytes / kernel time vs the 8 TB/s HBM peak) and the
-fp32 CPU restatement timed on this host as a reference point.
+decode kernel (algorithmic bytes / kernel time vs the 8 TB/s HBM peak), the
+ceiling of the call's own memory access pattern and the NT read stream, both
+measured in the same run with the kernels of libswiftllm_ceilings
+(include/swiftllm_ceilings.h), and the fp32 CPU restatement timed on this host
+as a reference point. `--ceiling X` times one of those kernels alone.
 
-The other configurations are measured the same way: --config 3 (8 sequences
-of 32768 tokens, 64 query heads, split-K), --config 4 (a ragged step: cache
-write of 256 new tokens, then decode) and --config 5 (MoE top-2 routing and
-dispatch of 4096 tokens, hidden 4096, 8 experts).
+The other configurations are measured the same way: --config 1 (the tiny MHA
+batch BASELINE states for the reference's CPU path; us/call, no roofline
+claim), --config 3 (8 sequences of 32768 tokens, 64 query heads, split-K),
+--config 4 (a ragged step: cache write of 256 new tokens, then decode),
+--config 5 (MoE top-2 routing and dispatch of 4096 tokens, hidden 4096, 8
+experts), and the "next" rows: --config 6/7 (block copies and swaps), 8 (the
+Mixtral MoE layer's expert GEMMs) and 9 (paged prefill).
 """
 
 from __future__ import annotations
@@ -64,7 +71,7 @@ def parse():
                     help="leave the live ceiling measurement out of the line (for profiles)")
     ap.add_argument("--partition", type=int, default=None,
                     help="v2 partition size in tokens, 0 = balanced (stream-K) scheduling; "
-                         "default 4096 for config 3, 1024 for config 4")
+                         "default 4096 for configs 3 and 4")
     ap.add_argument("--rotate", type=int, default=None,
                     help="input copies rotated between calls (default 4 for decode, 8 for MoE)")
     ap.add_argument("--seed", type=int, default=0)
@@ -207,10 +214,11 @@ def main():
     if args.variant is None:
         args.variant = "v1" if args.config in (1, 2) else "v2"
     if args.partition is None:
-        # measured defaults: 4096-token partitions for config 3 (long uniform
-        # contexts); 1024 for config 4, where the step (cache write + decode)
-        # took 195 us against 200 us balanced and 216 us single pass
-        args.partition = 4096 if args.config == 3 else 1024
+        # measured defaults: 4096-token partitions for both. Config 3 (long
+        # uniform contexts): 165 us, the same as 8192. Config 4 (ragged), with
+        # the split-K items started longest first: 175.7 us, against 177.4 at
+        # 2048, 182.0 at 1024 and 189.0 balanced
+        args.partition = 4096
     t0 = time.time()
     w = workloads.decode_config(args.config, seed=args.seed)
     sh = w.shape

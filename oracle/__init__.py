@@ -36,13 +36,16 @@ it (tests/test_oracle_*.py); every function here has at least one.
 from __future__ import annotations
 
 import ctypes
+import os
 import subprocess
 from pathlib import Path
 
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIB_PATH = HERE / "liboracle.so"
+# SWIFTLLM_ORACLE_LIB names another build (the sanitized one, `make -C oracle
+# sanitize`); by default liboracle.so here.
+LIB_PATH = Path(os.environ.get("SWIFTLLM_ORACLE_LIB") or HERE / "liboracle.so")
 
 _LIB = None
 

@@ -5,10 +5,13 @@ include/swiftllm_hip.h. The library is required: there is no fallback path.
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 from typing import Optional
 
-LIB_PATH = Path(__file__).resolve().parent / "libswiftllm_hip.so"
+# SWIFTLLM_HIP_LIB names another build of the library (the host-sanitized one
+# of swiftllm_amd/sanitize.py); by default the one next to this file.
+LIB_PATH = Path(os.environ.get("SWIFTLLM_HIP_LIB") or Path(__file__).resolve().parent / "libswiftllm_hip.so")
 
 _LIB: Optional[ctypes.CDLL] = None
 

@@ -9,10 +9,12 @@ this library.
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 from typing import Optional
 
-LIB_PATH = Path(__file__).resolve().parent / "libswiftllm_ceilings.so"
+LIB_PATH = Path(os.environ.get("SWIFTLLM_CEILINGS_LIB")
+                or Path(__file__).resolve().parent / "libswiftllm_ceilings.so")
 
 vp = ctypes.c_void_p
 i32 = ctypes.c_int
