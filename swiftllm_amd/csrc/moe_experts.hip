@@ -45,12 +45,18 @@ constexpr int kBW = 256;        // weight rows per workgroup tile (gated: 128 ga
 constexpr int kBK = 64;         // k per LDS stage: one 128-byte line of each tile row
 constexpr int kKMult = 64;      // k must be a multiple of this (the API's contract)
 constexpr int kMaxK = 1 << 21;  // k limit of the 32-bit buffer offsets
-constexpr int kStages = 2;      // LDS stages: one in flight while one is multiplied
+constexpr int kAStages = 2;     // LDS buffers of the activation tile: one stage in flight
+constexpr int kWStages = 3;     // LDS buffers of the weight tile: two stages in flight
 constexpr int kThreads = 512;   // 8 waves: 2 (rows) x 4 (weight rows), 128 x 64 each
 constexpr int kRowChunks = kBK / 8;                        // 16-byte chunks per tile row
 constexpr int kTileChunks = kBM * kRowChunks;              // chunks per operand tile
 constexpr int kLoads = kTileChunks / kThreads;             // direct loads per thread per tile
-constexpr size_t kStageHalfs = static_cast<size_t>(kBM + kBW) * kBK;
+constexpr size_t kTileHalfs = static_cast<size_t>(kBM) * kBK;  // one operand tile of a stage
+static_assert(kBM == kBW, "activation and weight tiles share one LDS buffer size");
+// LDS: activation buffers, then weight buffers, 32 KiB each: 160 KiB, all of
+// a CU's LDS. The expert tile table sits in the last weight buffer until the
+// main loop first writes there.
+constexpr size_t kLdsHalfs = (kAStages + kWStages) * kTileHalfs;
 constexpr int kMaxE = 256;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kXcds = 8;                 // MI355X: 8 XCDs, each with its own L2
@@ -95,7 +101,9 @@ constexpr int tile_cols() { return GATED ? kBW / 2 : kBW; }
 template <bool GATED>
 __global__ __launch_bounds__(kThreads) void moe_expert_gemm_kernel(const GemmArgs a) {
     extern __shared__ __align__(16) f16 lds[];
-    __shared__ int s_tile0[kMaxE + 1];  // first global row tile of each expert
+    // First global row tile of each expert, in the last weight buffer (free
+    // until the main loop loads its first stage there, after a barrier).
+    int* s_tile0 = reinterpret_cast<int*>(lds + (kAStages + kWStages - 1) * kTileHalfs);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar LDS addresses
@@ -146,8 +154,8 @@ __global__ __launch_bounds__(kThreads) void moe_expert_gemm_kernel(const GemmArg
     if (row0 < 0 || row0 >= row_end) return;
     const int col0 = nt * tile_cols<GATED>();
 
-    // LDS: kStages stages, each the activation tile [kBM][kBK] and the weight
-    // tile [kBW][kBK]. A row's 16-byte chunk c lives at chunk slot
+    // LDS: kAStages buffers of the activation tile [kBM][kBK], then kWStages
+    // of the weight tile [kBW][kBK]. A row's 16-byte chunk c lives at chunk slot
     // c ^ ((row / 2) % 8) of the row, so the 16 rows an MFMA operand read
     // serves at once fall in 16 different bank groups (rows are 128 bytes:
     // row parity picks the half of the 64 banks, the slot the group).
@@ -195,25 +203,35 @@ __global__ __launch_bounds__(kThreads) void moe_expert_gemm_kernel(const GemmArg
     // loads j < kLoads / 2 fill the gate rows and the others the up rows.
     auto issue_load = [&](int ks_idx, int j, bool w) {
         const unsigned soff = static_cast<unsigned>(min(ks_idx, nk - 1)) * kBK * 2u;
-        f16* lx = lds + static_cast<size_t>(ks_idx % kStages) * kStageHalfs;
         const int first = (j * (kThreads / 64) + wv) * 64;  // chunk slot of lane 0
         if (w) {
+            f16* lx = lds + static_cast<size_t>(kAStages + ks_idx % kWStages) * kTileHalfs;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                (GATED && j >= kLoads / 2) ? rw2 : rw,
-                to_lds(lx + (kBM * kBK + first * 8)),
+                (GATED && j >= kLoads / 2) ? rw2 : rw, to_lds(lx + first * 8),
                 16, woff[j], soff, 0, 0);
         } else {
+            f16* lx = lds + static_cast<size_t>(ks_idx % kAStages) * kTileHalfs;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 ra, to_lds(lx + first * 8), 16,
                 aoff[j], soff, 0, 0);
         }
     };
+    // Stage s + 1 of the activation tile, then stage s + 2 of the weight tile.
+    auto issue_stage = [&](int ka, int kw) {
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j) issue_load(ka, j, false);
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j) issue_load(kw, j, true);
+    };
     // Waits until this thread's loads of the stage about to be multiplied
-    // landed (loads of the kStages - 2 later stages stay in flight) and its
-    // LDS reads are done, then a bare barrier. The empty asm statements keep
-    // the compiler from moving LDS reads across it.
+    // landed and its LDS reads are done, then a bare barrier. Loads are
+    // issued a stage at a time, the activation tile's (stage s + 1) before the
+    // weight tile's (stage s + 2), so when stage s is due the only loads of
+    // this thread that may still be in flight are the kLoads weight loads of
+    // stage s + 1. The empty asm statements keep the compiler from moving LDS
+    // reads across the barrier.
     auto stage_ready = [&]() {
-        constexpr int vm = 2 * kLoads * (kStages - 2);
+        constexpr int vm = kLoads;
         __builtin_amdgcn_s_waitcnt((0x7 << 4) | (vm & 0xF) | ((vm >> 4) << 14));  // lgkmcnt(0)
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
@@ -232,27 +250,24 @@ __global__ __launch_bounds__(kThreads) void moe_expert_gemm_kernel(const GemmArg
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f16x{};
 
+    // Prologue: activation stage 0, weight stages 0 and 1 (in that order:
+    // the activation loads first, as stage_ready counts).
 #pragma unroll
-    for (int st = 0; st < kStages - 1; ++st)
+    for (int j = 0; j < kLoads; ++j) issue_load(0, j, false);
 #pragma unroll
-        for (int j = 0; j < kLoads; ++j) {
-            issue_load(st, j, false);
-            issue_load(st, j, true);
-        }
+    for (int j = 0; j < kLoads; ++j) issue_load(0, j, true);
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j) issue_load(1, j, true);
     const int lr = lane & 31;          // MFMA row / column within a 32 tile
     const int lc = lane >> 5;          // which 8 of the 16 k of an MFMA step
     for (int kt = 0; kt < nk; ++kt) {
         // Stage kt landed in every wave's share; every wave is done with
-        // stage kt - 1, whose buffer then takes stage kt + 1, which loads
-        // while stage kt is multiplied.
+        // stage kt - 1, whose buffers then take activation stage kt + 1 and
+        // weight stage kt + 2, which load while stage kt is multiplied.
         stage_ready();
-#pragma unroll
-        for (int j = 0; j < kLoads; ++j) {
-            issue_load(kt + kStages - 1, j, false);
-            issue_load(kt + kStages - 1, j, true);
-        }
-        const f16* bx = lds + static_cast<size_t>(kt % kStages) * kStageHalfs;
-        const f16* bw = bx + kBM * kBK;
+        issue_stage(kt + 1, kt + 2);
+        const f16* bx = lds + static_cast<size_t>(kt % kAStages) * kTileHalfs;
+        const f16* bw = lds + static_cast<size_t>(kAStages + kt % kWStages) * kTileHalfs;
 #pragma unroll
         for (int ks = 0; ks < kBK / 16; ++ks) {
             const int c = 2 * ks + lc;
@@ -397,10 +412,10 @@ int swiftllm_hip_moe_expert_gemm(const void* a, const void* w, const void* w2,
     if (grid > 0x7fffffffLL) {
         return fail(SWIFTLLM_ERR_NOT_SUPPORTED, "%s: %lld tiles", who, grid);
     }
-    // Dynamic LDS: kStages stages of the activation and weight tiles
-    // (128 KiB), above the default limit, so the limit is raised.
+    // Dynamic LDS: the activation and weight buffers (160 KiB), above the
+    // default limit, so the limit is raised.
     const bool gated = (w2 != nullptr);
-    const size_t lds = kStages * kStageHalfs * sizeof(f16);
+    const size_t lds = kLdsHalfs * sizeof(f16);
     const void* fn = gated ? reinterpret_cast<const void*>(moe_expert_gemm_kernel<true>)
                            : reinterpret_cast<const void*>(moe_expert_gemm_kernel<false>);
     hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
