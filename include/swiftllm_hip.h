@@ -398,6 +398,21 @@ int swiftllm_hip_gather_kv(const void* key_cache, const void* value_cache,
                            int max_num_blocks_per_seq, int max_context_len,
                            void* k_out, void* v_out, hipStream_t stream);
 
+/* Wave-reduction check: the lane reductions the kernels inline (the
+ * reference's 32-lane butterflies, paged_attention.cu:17-31, on 64-lane
+ * waves), run on caller data so they can be compared lane by lane with a
+ * sequential reference. For each row r < num_rows of x (float [num_rows][64])
+ * and xi (int32 [num_rows][64]), lane l writes
+ *   out[r][0][l] = max of x[r][l % 16 + 16 k], k = 0..3  (softmax row max)
+ *   out[r][1][l] = sum of the same four                  (softmax row sum)
+ *   out[r][2][l] = max of x[r][0..63]                    (split-K reduce)
+ *   out[r][3][l] = sum of x[r][0..63]
+ *   scan[r][l]   = xi[r][0] + ... + xi[r][l]             (dispatch offsets)
+ * out is float [num_rows][4][64], scan int32 [num_rows][64]. */
+int swiftllm_hip_wave_reduce_check(const float* x, const int32_t* xi,
+                                   int num_rows, float* out, int32_t* scan,
+                                   hipStream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* 6. Host-side metadata (no device work).                                   */
 /* ------------------------------------------------------------------------ */

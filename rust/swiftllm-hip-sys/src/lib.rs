@@ -228,6 +228,13 @@ extern "C" {
         max_context_len: c_int, k_out: *mut c_void, v_out: *mut c_void, stream: hipStream_t,
     ) -> c_int;
 
+    /// The lane reductions of the kernels on caller rows (max / sum over the
+    /// four 16-lane groups, over the wave, and the inclusive scan).
+    pub fn swiftllm_hip_wave_reduce_check(
+        x: *const c_float, xi: *const i32, num_rows: c_int, out: *mut c_float, scan: *mut i32,
+        stream: hipStream_t,
+    ) -> c_int;
+
     // -- host metadata: kv_cache.rs:186-216, 250-286 ------------------------------
     pub fn swiftllm_hip_slot_mapping(
         block_table: *const u64, table_len: usize, block_size: usize, start_pos: usize,

@@ -91,6 +91,7 @@ SIGNATURES = {
     "swiftllm_hip_moe_combine": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp]),
     "swiftllm_hip_gather_kv": (
         i32, [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp, vp, vp]),
+    "swiftllm_hip_wave_reduce_check": (i32, [vp, vp, i32, vp, vp, vp]),
     "swiftllm_hip_slot_mapping": (i32, [vp, sz, sz, sz, sz, vp]),
     "swiftllm_hip_pack_block_tables": (i32, [vp, vp, vp, sz, sz, sz, vp, vp]),
 }

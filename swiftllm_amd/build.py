@@ -24,7 +24,8 @@ LIB = PKG / "libswiftllm_hip.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["abi.cpp", "paged_attention.hip", "prefill.hip", "cache_ops.hip", "block_copy.hip", "moe.hip", "moe_experts.hip"]
+SOURCES = ["abi.cpp", "paged_attention.hip", "prefill.hip", "cache_ops.hip", "block_copy.hip", "moe.hip",
+           "moe_experts.hip", "checks.hip"]
 
 # The measurement kernels bench.py times beside the path (include/swiftllm_ceilings.h)
 # are a library of their own, outside the drop-in interface.

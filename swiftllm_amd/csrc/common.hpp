@@ -74,4 +74,30 @@ __host__ __device__ inline int kv_elem_offset(int d, int t) {
     return d * kBlockTokens + t;
 }
 
+// ---------------------------------------------------------------------------
+// Whole-wave reductions (wave64). Every lane ends with the same value; the
+// butterfly adds pairs in the same order in every lane.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d);
+        if (lane >= d) x += y;
+    }
+    return x;
+}
+
 }  // namespace swiftllm

@@ -187,16 +187,6 @@ __device__ __forceinline__ void rank_chunk(const int (&id)[K], int (&rk)[K], int
     }
 }
 
-// Inclusive prefix sum over the 64 lanes of a wave.
-__device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int y = __shfl_up(x, d);
-        if (lane >= d) x += y;
-    }
-    return x;
-}
-
 // ---------------------------------------------------------------------------
 // (1) Rank, optionally after routing.
 // ---------------------------------------------------------------------------

@@ -113,15 +113,16 @@ __device__ __forceinline__ void attend_blocks(WaveState<D>& st, const const_int*
     }
 }
 
-// Longest-first dispatch: workgroups are issued roughly in blockIdx order, so
-// blockIdx.z = r serves the sequence with the r-th longest context (ties by
-// index). Long sequences start first and short ones fill in at the end.
-// Sequence counts above kLptMaxSeqs keep the identity order (the O(S^2)
-// ranking below would cost more than it saves).
-#ifndef SWIFTLLM_LPT_MAX_SEQS
-#define SWIFTLLM_LPT_MAX_SEQS 1024
-#endif
-constexpr int kLptMaxSeqs = SWIFTLLM_LPT_MAX_SEQS;
+// The sequence with the r-th longest context (ties by index), found by every
+// workgroup of a single-pass grid that is resident all at once (the snake
+// order below). Each thread ranks S / 256 sequences against all S, so the
+// cost grows as S^2: measured on MI355X with the ranking in every grid,
+// 1024 sequences of 32-128 tokens took 1324 us against 67 us in plain order,
+// and 256 of them 39.7 against 18.8 us. So only batches of up to
+// kLptMaxSeqs sequences are ranked (at most 128 compares a thread), and larger
+// grids run in sequence order, which the dispatcher balances as workgroups
+// finish.
+constexpr int kLptMaxSeqs = 128;
 
 __device__ __forceinline__ int sequence_for_block(const int* ctx, int S, int r) {
     if (S > kLptMaxSeqs) return r;
@@ -295,7 +296,7 @@ void paged_decode_kernel(const DecodeArgs a) {
     } else {
         kvh = blockIdx.y / a.nhc;
         hc = blockIdx.y - kvh * a.nhc;
-        s = sequence_for_block(a.ctx, gridDim.z, blockIdx.z);
+        s = blockIdx.z;
     }
     decode_item<D, NW>(a, s, kvh, hc, 0);
 }
@@ -484,18 +485,6 @@ void paged_partition_kernel(const DecodeArgs a) {
 // aligned); out(d, v) stores one output.
 constexpr int kReduceThreads = 256;
 constexpr int kReduceChunk = 1024;  // fragment weights staged in LDS per pass
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-    return v;
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    return v;
-}
 
 template <int D, typename FM, typename FL, typename FO, typename OUT>
 __device__ __forceinline__ void combine_head(int P, FM fm, FL fl, FO fo, OUT out) {
@@ -1104,10 +1093,10 @@ int decode_v1(void* out, const void* q, const void* kc, const void* vc, const in
     DecodeArgs a = make_args(out, q, kc, vc, bt, ctx, scale, sh, num_blocks);
     a.part_blocks = 0;
     a.MP = 1;
-    // Snake order when the whole grid is resident at once (three 4-wave
-    // workgroups per CU at the kernel's register count) and sequences are
-    // ranked; otherwise plain longest-first order for the dispatcher to
-    // balance dynamically.
+    // Snake order over the ranked sequences when the whole grid is resident
+    // at once (three 4-wave workgroups per CU at the kernel's register count)
+    // and small enough to rank; otherwise sequence order, balanced by the
+    // dispatcher as workgroups finish.
     const long long items = static_cast<long long>(sh.S) * a.Hkv * a.nhc;
     a.snake = (kWavesV1 == 4 && sh.S <= kLptMaxSeqs && items <= 3LL * device_cus()) ? device_cus() : 0;
     return launched(launch_decode<kWavesV1>(a, sh.D, sh.S, 1, stream), who);

@@ -353,7 +353,7 @@ def test_one_long_sequence_many_fragments(dev, G):
 
 def test_more_sequences_than_the_lds_tables(dev):
     """4500 short sequences: the single pass drops its longest-first ranking
-    (more than 1024 sequences), the partition kernel takes one item per
+    (more than 128 sequences), the partition kernel takes one item per
     workgroup over the full grid (more than 4096), and balanced mode falls
     back to 512-token partitions (more than 4096)."""
     rng = np.random.default_rng(45)
