@@ -60,10 +60,11 @@ def parse():
                          "9: Llama-3-8B paged prefill (8 prompts of 2048 tokens)")
     ap.add_argument("--variant", choices=["v1", "v2"], default=None,
                     help="default: v1 for configs 1 and 2, v2 for configs 3 and 4")
-    ap.add_argument("--ceiling", choices=["stream", "gather", "store", "rowcopy"], default=None,
-                    help="time one access-pattern ceiling kernel alone (libswiftllm_ceilings) and print "
-                         "its JSON line: the NT read stream; config 2/3/4's tile gather (--load-bytes); "
-                         "config 4's cache-write stores (--store-mode); config 5's row copies")
+    ap.add_argument("--ceiling", choices=["stream", "gather", "store", "rowcopy", "mfma"], default=None,
+                    help="time one ceiling kernel alone (libswiftllm_ceilings) and print its JSON line: "
+                         "the NT read stream; config 2/3/4's tile gather (--load-bytes); config 4's "
+                         "cache-write stores (--store-mode); config 5's row copies; the expert GEMM's "
+                         "MFMA stream on random operands (TFLOP/s)")
     ap.add_argument("--load-bytes", type=int, choices=[8, 16], default=16, help="--ceiling gather")
     ap.add_argument("--store-mode", type=int, choices=[0, 1, 2], default=1,
                     help="--ceiling store: 0 four rows per lane, 1 one line per 4 lanes, 2 whole rows")
@@ -512,6 +513,40 @@ def measure_store(w, pools, slots, stream, steps, mode):
     return timed(step, stream, steps, 10, 0)[0] * 1e3
 
 
+# The MFMA stream's grid: the gated expert GEMM of config 8 (32 row tiles x
+# 112 column tiles of 256 x 128 outputs, k = 4096 in 64 stages of 64).
+MFMA_GROUPS, MFMA_STAGES = 32 * 112, 64
+
+
+def measure_mfma(stream, steps=10, seed=0):
+    """Dense fp16 MFMA rate this box sustains on random operands: the
+    expert GEMM's matrix instructions alone (libswiftllm_ceilings MFMA
+    stream) over the gated GEMM's grid. Returns (TFLOP/s, us per launch)."""
+    from swiftllm_amd import ceilings
+    from swiftllm_amd._hip import DeviceArray
+
+    rng = np.random.default_rng(seed)
+    ops = DeviceArray.from_numpy(rng.standard_normal(1 << 19).astype(np.float16))  # 1 MiB
+    sink = DeviceArray((1,), np.uint32)
+
+    def step(i):
+        ceilings.mfma_stream(ops, ops.nbytes, MFMA_GROUPS, MFMA_STAGES, sink, stream)
+
+    us = timed(step, stream, steps, 3, 0)[0] * 1e3
+    flop = ceilings.MFMA_FLOP_PER_GROUP_STAGE * MFMA_GROUPS * MFMA_STAGES
+    return flop / (us * 1e-6) / 1e12, us
+
+
+def mfma_ceiling(stream, no_ceiling):
+    if no_ceiling:
+        return None
+    tflops, us = measure_mfma(stream)
+    return {"pattern": "the expert GEMM's MFMA instructions alone (libswiftllm_ceilings MFMA stream: "
+                       "its grid, 8 waves per workgroup, 128 x 64 wave tiles of v_mfma_f32_32x32x16_f16, "
+                       "random fp16 operands in registers, no memory traffic)",
+            "value": round(tflops, 2), "unit": "TFLOP/s", "us_per_launch": round(us, 3)}
+
+
 def decode_ceiling(w, pools, bt, stream, steps, kv_bytes, partition_tokens, slots=None):
     """The access-pattern ceiling of a decode call: the tile gather at 8- and
     16-byte loads in the decode's own work items (the faster counts), plus
@@ -597,7 +632,7 @@ def bench_ceiling(args):
                  for _ in range(max(1, args.rotate or 4))]
         bt, ctx = DeviceArray.from_numpy(w.block_tables), DeviceArray.from_numpy(w.context_lens)
         if args.ceiling == "gather":
-            part = args.partition if args.partition is not None else {2: 0, 3: 4096, 4: 1024}[cfg]
+            part = args.partition if args.partition is not None else {2: 0, 3: 4096, 4: 4096}[cfg]
             us = measure_gather(w, pools, bt, stream, steps, args.load_bytes, part)
             nbytes = w.kv_bytes()
             work = {"workload": f"config{cfg}-tile-gather", "load_bytes": args.load_bytes,
@@ -613,6 +648,18 @@ def bench_ceiling(args):
                     "tokens": sh["num_seqs"], "bytes_written_per_call": nbytes,
                     "kv_pool_copies_rotated": len(pools)}
         gbs = nbytes / (us * 1e-6) / 1e9
+    elif args.ceiling == "mfma":
+        tflops, us = measure_mfma(stream, steps=max(args.steps // 10, 10), seed=args.seed)
+        rec = {"metric": "MFMA stream ceiling TFLOP/s (libswiftllm_ceilings)", "value": round(tflops, 2),
+               "unit": "TFLOP/s", "n_gpus": 1, "us_per_call": round(us, 3),
+               "mfma_peak_frac": round(tflops / 2500.0, 4), "higher_is_better": True,
+               "dtype": "f16 operands, f32 accumulate (v_mfma_f32_32x32x16_f16)",
+               "data": "synthetic (seeded standard normal fp16 operands)",
+               "config": {"workload": "expert-gemm-mfma-stream", "workgroups": MFMA_GROUPS,
+                          "stages": MFMA_STAGES, "waves_per_workgroup": 8,
+                          "flop_per_launch": ceilings.MFMA_FLOP_PER_GROUP_STAGE * MFMA_GROUPS * MFMA_STAGES}}
+        print(json.dumps(rec), flush=True)
+        return
     else:
         wl = workloads.moe_config(seed=args.seed)
         T, hidden = wl.x.shape
@@ -772,6 +819,9 @@ def bench_prefill(args):
                      "frac": round(tflops / 2500.0, 4), "traffic": None},
         "cpu_baseline": None,
     }
+    ceiling = mfma_ceiling(stream, args.no_ceiling)
+    rec["ceiling"] = ceiling
+    rec["ceiling_frac"] = round(tflops / ceiling["value"], 4) if ceiling else None
     print(json.dumps(rec), flush=True)
 
 
@@ -819,6 +869,9 @@ def bench_moe_mlp(args):
                      "frac": round(tflops / 2500.0, 4), "traffic": None},
         "cpu_baseline": None,
     }
+    ceiling = mfma_ceiling(stream, args.no_ceiling)
+    rec["ceiling"] = ceiling
+    rec["ceiling_frac"] = round(tflops / ceiling["value"], 4) if ceiling else None
     print(json.dumps(rec), flush=True)
 
 

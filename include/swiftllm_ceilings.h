@@ -17,7 +17,11 @@
  *                  into each 32-byte row of each touched tile, without the
  *                  loads (or, for comparison, whole 32-byte rows);
  *   row copy       the MoE permute's copies: each row read once and written
- *                  to top_k destination rows with nontemporal stores.
+ *                  to top_k destination rows with nontemporal stores;
+ *   mfma stream    the expert GEMM's matrix instructions alone (its grid,
+ *                  waves per SIMD, wave tile and MFMA form) on random fp16
+ *                  operands held in registers: the dense fp16 rate this
+ *                  box sustains at the clock that much matrix work allows.
  *
  * Return values: 0 on success, -4 for invalid arguments, -6 for unsupported
  * shapes, -2 when the launch fails (the codes of include/swiftllm_hip.h).
@@ -82,6 +86,15 @@ int swiftllm_ceil_cache_store(void* key_cache, void* value_cache,
 int swiftllm_ceil_row_copy(const void* src, void* dst, const int32_t* dst_rows,
                            int num_tokens, int top_k, int hidden,
                            int num_dst_rows, hipStream_t stream);
+
+/* num_groups workgroups of 8 waves, each wave issuing `stages` x 32
+ * v_mfma_f32_32x32x16_f16 (4 k steps of a 128 x 64 tile per 64-k stage:
+ * 2 * 32 * 32 * 16 * 32 FLOP per wave per stage) on operands read once from
+ * `operands` (operand_bytes >= 1024, 16-byte aligned; fill it with random
+ * fp16 like the GEMM's data). */
+int swiftllm_ceil_mfma_stream(const void* operands, size_t operand_bytes,
+                              int num_groups, int stages, uint32_t* sink,
+                              hipStream_t stream);
 
 #ifdef __cplusplus
 }

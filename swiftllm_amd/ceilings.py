@@ -25,7 +25,12 @@ SIGNATURES = {
     "swiftllm_ceil_tile_gather": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]),
     "swiftllm_ceil_cache_store": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, vp]),
     "swiftllm_ceil_row_copy": (i32, [vp, vp, vp, i32, i32, i32, i32, vp]),
+    "swiftllm_ceil_mfma_stream": (i32, [vp, sz, i32, i32, vp, vp]),
 }
+
+# FLOP of one workgroup-stage of the MFMA stream: 8 waves x 32
+# v_mfma_f32_32x32x16_f16 of 2 * 32 * 32 * 16 FLOP.
+MFMA_FLOP_PER_GROUP_STAGE = 8 * 32 * 2 * 32 * 32 * 16
 
 # cache_store modes
 STORE_4_ROWS_PER_LANE = 0   # each thread: four 2-byte stores to rows d .. d+3
@@ -71,6 +76,11 @@ def cache_store(kc, vc, slots, num_tokens: int, num_kv_heads: int, head_dim: int
                 num_blocks: int, mode: int, stream=None) -> None:
     _check(lib().swiftllm_ceil_cache_store(kc.ptr, vc.ptr, slots.ptr, num_tokens, num_kv_heads,
                                            head_dim, num_blocks, mode, _h(stream)), "cache_store")
+
+
+def mfma_stream(operands, nbytes: int, num_groups: int, stages: int, sink, stream=None) -> None:
+    _check(lib().swiftllm_ceil_mfma_stream(operands.ptr, nbytes, num_groups, stages, sink.ptr,
+                                           _h(stream)), "mfma_stream")
 
 
 def row_copy(src, dst, dst_rows, num_tokens: int, top_k: int, hidden: int, num_dst_rows: int,

@@ -5,7 +5,8 @@
 //
 // Every load feeds an XOR fold whose result is stored only when it equals a
 // fixed constant, so the compiler keeps every load and the kernels write
-// (almost) nothing but what the pattern itself writes.
+// (almost) nothing but what the pattern itself writes. The one compute
+// pattern, the MFMA stream, folds its accumulators the same way.
 
 #include <hip/hip_runtime.h>
 
@@ -246,6 +247,69 @@ __global__ __launch_bounds__(256) void row_copy_kernel(const CopyArgs a) {
     }
 }
 
+// MFMA stream: the expert GEMM's matrix work with no memory traffic in the
+// loop. Workgroups of 8 waves (two per SIMD, the GEMM's occupancy); per
+// 64-k stage each wave issues 4 k steps of 8 v_mfma_f32_32x32x16_f16 into
+// 8 accumulators (the GEMM's 128 x 64 wave tile). The 4 steps use 4
+// different operand sets, loaded once from random fp16 the caller provides,
+// so successive MFMAs see different data as they do in the GEMM: the
+// matrix cores' power, and so the clock they sustain, depends on the data
+// (constant operands run faster than random ones).
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f16x __attribute__((ext_vector_type(16)));
+constexpr int kMfmaWaves = 8;
+constexpr int kMfmaSteps = 4;  // k steps of 16 per 64-k stage
+constexpr float kMfmaSinkValue = 1.2345678e30f;
+
+struct MfmaArgs {
+    const h8* ops;  // n_ops fragments of 64 lanes x 8 halves
+    uint32_t* sink;
+    int n_ops;
+    int stages;
+};
+
+__global__ __launch_bounds__(64 * kMfmaWaves) void mfma_stream_kernel(const MfmaArgs a) {
+    const int lane = threadIdx.x % 64;
+    const int wv = threadIdx.x / 64;
+    const long long base = (static_cast<long long>(blockIdx.x) * kMfmaWaves + wv) * kMfmaSteps * 6;
+    h8 x[kMfmaSteps][4], w[kMfmaSteps][2];
+#pragma unroll
+    for (int s = 0; s < kMfmaSteps; ++s) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            x[s][j] = a.ops[((base + s * 6 + j) % a.n_ops) * 64 + lane];
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            w[s][i] = a.ops[((base + s * 6 + 4 + i) % a.n_ops) * 64 + lane];
+        }
+    }
+    f16x acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f16x{};
+    for (int st = 0; st < a.stages; ++st) {
+#pragma unroll
+        for (int s = 0; s < kMfmaSteps; ++s)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w[s][i], x[s][j], acc[i][j], 0, 0, 0);
+    }
+    // A float sum: hipcc (ROCm 7.2) drops the whole kernel when the
+    // accumulators are folded by their bit patterns instead.
+    float f = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) f += acc[i][j][r];
+    if (f == kMfmaSinkValue) *a.sink = kSinkMagic;
+}
+
 }  // namespace
 }  // namespace swiftllm_ceilings
 
@@ -309,6 +373,16 @@ int swiftllm_ceil_row_copy(const void* src, void* dst, const int32_t* dst_rows, 
     CopyArgs a{static_cast<const u32x4*>(src), static_cast<u32x4*>(dst), dst_rows, num_tokens, top_k,
                hidden / 8, num_dst_rows};
     return launch(row_copy_kernel, dim3((num_tokens + 3) / 4), dim3(256), stream, a);
+}
+
+int swiftllm_ceil_mfma_stream(const void* operands, size_t operand_bytes, int num_groups,
+                              int stages, uint32_t* sink, hipStream_t stream) {
+    if (num_groups < 0 || stages < 0 || !operands || !sink || !aligned(operands, 16)) return kErrInvalid;
+    const long long n_ops = static_cast<long long>(operand_bytes / (64 * sizeof(h8)));
+    if (n_ops < 1 || n_ops > 0x7fffffffLL) return kErrInvalid;
+    if (num_groups == 0 || stages == 0) return kOk;
+    MfmaArgs a{static_cast<const h8*>(operands), sink, static_cast<int>(n_ops), stages};
+    return launch(mfma_stream_kernel, dim3(num_groups), dim3(64 * kMfmaWaves), stream, a);
 }
 
 }  // extern "C"

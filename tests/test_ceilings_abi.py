@@ -21,7 +21,7 @@ def _declared():
 def test_exports_every_declared_function():
     L = ceilings.lib()
     names = _declared()
-    assert len(names) == 4
+    assert len(names) == 5
     assert sorted(ceilings.SIGNATURES) == names
     assert all(hasattr(L, n) for n in names)
 
@@ -43,8 +43,12 @@ def test_validation_before_launch():
                                        None) == -6                                # 4-byte loads
     assert L.swiftllm_ceil_cache_store(FAKE, FAKE, FAKE, 4, 8, 128, 0, 3, None) == -4  # mode 3
     assert L.swiftllm_ceil_row_copy(FAKE, FAKE, FAKE, 4, 2, 4000, 8, None) == -6  # hidden % 512
+    assert L.swiftllm_ceil_mfma_stream(FAKE, 512, 4, 4, FAKE, None) == -4         # < one fragment
+    assert L.swiftllm_ceil_mfma_stream(FAKE + 8, 4096, 4, 4, FAKE, None) == -4    # misaligned
+    assert L.swiftllm_ceil_mfma_stream(FAKE, 4096, -1, 4, FAKE, None) == -4       # negative grid
     for fn, args in [(L.swiftllm_ceil_read_stream, (FAKE, 0, FAKE, None)),
-                     (L.swiftllm_ceil_row_copy, (FAKE, FAKE, FAKE, 0, 2, 4096, 8, None))]:
+                     (L.swiftllm_ceil_row_copy, (FAKE, FAKE, FAKE, 0, 2, 4096, 8, None)),
+                     (L.swiftllm_ceil_mfma_stream, (FAKE, 4096, 0, 64, FAKE, None))]:
         assert fn(*args) == 0                                                     # nothing to do
 
 
