@@ -36,6 +36,14 @@ __device__ __forceinline__ const const_int* as_const(const int* p) {
     return (const const_int*)(p);
 }
 
+// Direct memory-to-LDS loads through buffer resources (buffer_load ... lds):
+// the resource's base and size are wave-uniform, the lane's byte offset 32
+// bits. The compiler adds no waits of its own between these loads and LDS
+// reads; every kernel that issues them waits for its loads explicitly.
+constexpr int kRsrcWord3 = 0x00020000;   // gfx9 buffer resource: raw 32-bit dwords
+typedef __attribute__((address_space(3))) void* lds_ptr;
+__device__ __forceinline__ lds_ptr to_lds(void* p) { return (lds_ptr)p; }
+
 inline bool aligned(const void* p, size_t bytes) {
     return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
 }

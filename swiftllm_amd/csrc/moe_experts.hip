@@ -67,7 +67,6 @@ constexpr int kXcds = 8;                 // MI355X: 8 XCDs, each with its own L2
 constexpr int kSuperMGated = 8;
 constexpr int kSuperMPlain = 16;
 constexpr int kSuper = 32;
-constexpr int kRsrcWord3 = 0x00020000;   // gfx9 buffer resource: raw 32-bit dwords
 
 struct GemmArgs {
     const f16* a;        // [m_total][k]
@@ -84,9 +83,6 @@ struct GemmArgs {
     int sm;              // super-tiles along the rows
     int super_m;         // row tiles per super-tile (column tiles: kSuper / super_m)
 };
-
-typedef __attribute__((address_space(3))) void* lds_ptr;
-__device__ __forceinline__ lds_ptr to_lds(f16* p) { return (lds_ptr)p; }
 
 __device__ __forceinline__ f16x mfma32(h8 a, h8 b, f16x c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
