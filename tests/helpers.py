@@ -1,5 +1,5 @@
-"""Shared helpers for the tests: running the library on numpy inputs and the
-attention tolerance of the decode path."""
+"""Shared helpers for the tests: running the library on numpy inputs, the
+attention tolerance of the decode path and the expert GEMM's tolerance."""
 
 from __future__ import annotations
 
@@ -32,6 +32,31 @@ def assert_attention_close(out, ref, what=""):
         f"{what}: max_abs={max_abs:.3e} (<= {ATOL}) max_rel={max_rel:.3e} (<= {RTOL}) "
         f"norm_rel={norm_rel:.3e}")
     return max_abs, max_rel, norm_rel
+
+
+def assert_gemm_close(gpu, ref, what=""):
+    """Expert GEMM tolerance: fp16 outputs of fp32 accumulation against
+    float64 on the same fp16 inputs, |gpu - ref| <= 2^-10 |ref| + 1e-3
+    rms(ref) (one fp16 rounding plus fp32 accumulation; an indexing mistake
+    is off by O(rms))."""
+    gpu = np.asarray(gpu, np.float64)
+    assert np.all(np.isfinite(gpu)), what
+    rms = float(np.sqrt(np.mean(ref ** 2))) if ref.size else 0.0
+    err = np.abs(gpu - ref)
+    bound = 2.0 ** -10 * np.abs(ref) + 1e-3 * rms
+    worst = float((err - bound).max()) if err.size else -1.0
+    assert worst <= 0, f"{what}: max err {err.max():.3e}, rms {rms:.3e}"
+
+
+def expert_offsets(rng, E, m_total, empty=()):
+    """Offsets of E experts over m_total rows cut at random points; the rows
+    of each expert in `empty` move to the next one."""
+    cuts = np.sort(rng.integers(0, m_total + 1, size=E - 1))
+    counts = np.diff(np.concatenate([[0], cuts, [m_total]]))
+    for e in empty:
+        counts[(e + 1) % E] += counts[e]
+        counts[e] = 0
+    return np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
 
 
 class DeviceWorkload:

@@ -12,29 +12,12 @@ import numpy as np
 import pytest
 
 import oracle
+from helpers import assert_gemm_close as _close
+from helpers import expert_offsets as _offsets
 from swiftllm_amd import moe, workloads
 from swiftllm_amd._hip import DeviceArray, synchronize
 
 pytestmark = pytest.mark.gpu
-
-
-def _close(gpu, ref, what):
-    gpu = np.asarray(gpu, np.float64)
-    assert np.all(np.isfinite(gpu)), what
-    rms = float(np.sqrt(np.mean(ref ** 2))) if ref.size else 0.0
-    err = np.abs(gpu - ref)
-    bound = 2.0 ** -10 * np.abs(ref) + 1e-3 * rms
-    worst = float((err - bound).max()) if err.size else -1.0
-    assert worst <= 0, f"{what}: max err {err.max():.3e}, rms {rms:.3e}"
-
-
-def _offsets(rng, E, m_total, empty=()):
-    cuts = np.sort(rng.integers(0, m_total + 1, size=E - 1))
-    counts = np.diff(np.concatenate([[0], cuts, [m_total]]))
-    for e in empty:  # move an expert's rows to the next one
-        counts[(e + 1) % E] += counts[e]
-        counts[e] = 0
-    return np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
 
 
 @pytest.mark.parametrize("gated", [False, True])

@@ -12,9 +12,13 @@ rerun exactly.
            oracle.prefill_numpy, NaN in unused slots
   moe      route + dispatch: expert ids, counts, offsets, inverse index,
            sorted ids and permuted rows bit-exact, weights within 1e-6
+  experts  the grouped expert GEMM, plain and gated, over random expert
+           counts (empty experts and 1-row tails included): the GEMM
+           tolerance against oracle.moe_expert_gemm
 
-Tolerance (fp16 in/out, fp32 accumulation): max abs error <= 2e-3 and max
-relative error <= 1e-2 with a 1e-3 floor on |ref| (tests/helpers.py).
+Tolerances (tests/helpers.py): attention, max abs error <= 2e-3 and max
+relative error <= 1e-2 with a 1e-3 floor on |ref|; expert GEMM, |gpu - ref| <=
+2^-10 |ref| + 1e-3 rms(ref).
 """
 
 import dataclasses
@@ -23,7 +27,7 @@ import numpy as np
 import pytest
 
 import oracle
-from helpers import DeviceWorkload, assert_attention_close
+from helpers import DeviceWorkload, assert_attention_close, assert_gemm_close, expert_offsets
 from swiftllm_amd import moe
 from swiftllm_amd import paged_attention as pa
 from swiftllm_amd import workloads
@@ -141,3 +145,26 @@ def test_moe_route_dispatch_random(dev, seed):
     nrows = int(offsets[-1])
     assert np.array_equal(bufs.sorted_token_ids.numpy()[:nrows], sorted_ids), what
     assert np.array_equal(bufs.x_perm.numpy()[:nrows].view(np.uint16), x[sorted_ids].view(np.uint16)), what
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_expert_gemm_random(dev, seed):
+    rng = np.random.default_rng(5000 + seed)
+    gated = bool(rng.integers(2))
+    E = int(rng.integers(1, 13))
+    m_total = int(rng.choice([1, 255, 257, 700, 1500]))
+    n = (128 if gated else 256) * int(rng.integers(1, 5))
+    k = 64 * int(rng.integers(1, 17))
+    empty = tuple(int(e) for e in rng.choice(E, size=min(E - 1, int(rng.integers(0, 3))), replace=False))
+    offs = expert_offsets(rng, E, m_total, empty=empty)
+    a = (rng.standard_normal((m_total, k)) * 0.5).astype(np.float16)
+    w = (rng.standard_normal((E, n, k)) / np.sqrt(k)).astype(np.float16)
+    w2 = (rng.standard_normal((E, n, k)) / np.sqrt(k)).astype(np.float16) if gated else None
+    c = DeviceArray((m_total, n), np.float16)
+    c.fill_byte(0xFF)
+    moe.moe_expert_gemm(DeviceArray.from_numpy(a), DeviceArray.from_numpy(w),
+                        DeviceArray.from_numpy(w2) if gated else None, DeviceArray.from_numpy(offs), c)
+    synchronize()
+    assert_gemm_close(c.numpy(), oracle.moe_expert_gemm(a, w, w2, offs),
+                      f"seed {5000 + seed}: gated={gated} E={E} rows={m_total} n={n} k={k} "
+                      f"counts {list(np.diff(offs))}")
