@@ -29,7 +29,9 @@
 //   workgroups exit at once.
 // combine: out[t, :] = sum_k weights[t, k] * y[inverse[t, k], :] in fp32
 //   (k ascending, fused multiply-add), rounded once to fp16; entries with
-//   inverse -1 contribute nothing.
+//   inverse outside [0, rows of y) contribute nothing. One wave per token;
+//   for top-k <= 8 (except 5 and 7) a kernel with k fixed at compile time
+//   issues all of a lane's row loads for several chunks before adding.
 
 #include "common.hpp"
 
@@ -369,6 +371,63 @@ struct CombineArgs {
     int rows;            // rows of y (bound on inverse)
 };
 
+// Top-k known at compile time (KC = K <= 8). The bound is bytes in flight, so
+// each lane issues the loads of U row chunks of all KC rows before the first
+// multiply-add: 16·U·KC bytes per lane. Each row of y is read exactly once per
+// call, so the loads are nontemporal. A row index outside [0, rows) gives no
+// term: its load reads row 0 (rows > 0 on this path), and the term becomes
+// 0 · (−0) = −0, which leaves every accumulator bit for bit as it was, so
+// the loads need no branches. Terms add in k order in fp32, then
+// one fp16 rounding, as in the generic kernel below.
+template <int KC>
+__global__ __launch_bounds__(256) void moe_combine_kernel_k(const CombineArgs a) {
+    constexpr int U = KC <= 2 ? 4 : (KC <= 4 ? 2 : 1);
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= a.T) return;
+    const int nv = a.hidden / 8;
+    const h8* src[KC];
+    float w[KC];
+    bool use[KC];
+#pragma unroll
+    for (int k = 0; k < KC; ++k) {
+        const int row = a.inverse[static_cast<size_t>(t) * KC + k];
+        use[k] = row >= 0 && row < a.rows;
+        w[k] = use[k] ? a.wts[static_cast<size_t>(t) * KC + k] : 0.0f;
+        src[k] = reinterpret_cast<const h8*>(a.y + static_cast<size_t>(use[k] ? row : 0) * a.hidden);
+    }
+    h8* dst = reinterpret_cast<h8*>(a.out + static_cast<size_t>(t) * a.hidden);
+    for (int i0 = lane; i0 < nv; i0 += 64 * U) {
+        h8 v[U][KC];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int i = min(i0 + 64 * u, nv - 1);
+#pragma unroll
+            for (int k = 0; k < KC; ++k) v[u][k] = __builtin_nontemporal_load(src[k] + i);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (i0 + 64 * u >= nv) break;
+            float acc[8];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) acc[r] = 0.0f;
+#pragma unroll
+            for (int k = 0; k < KC; ++k) {
+#pragma unroll
+                for (int r = 0; r < 8; ++r) {
+                    acc[r] = __builtin_fmaf(w[k], use[k] ? static_cast<float>(v[u][k][r]) : -0.0f,
+                                            acc[r]);
+                }
+            }
+            h8 o;
+#pragma unroll
+            for (int r = 0; r < 8; ++r) o[r] = static_cast<f16>(acc[r]);
+            dst[i0 + 64 * u] = o;
+        }
+    }
+}
+
+// Any top-k: one row load in flight per lane.
 __global__ __launch_bounds__(256) void moe_combine_kernel(const CombineArgs a) {
     const int lane = threadIdx.x & 63;
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -487,8 +546,18 @@ int swiftllm_hip_moe_combine(const void* y, const float* weights, const int32_t*
     if (num_tokens == 0) return ok();
     CombineArgs g{static_cast<const f16*>(y), weights, inverse, static_cast<f16*>(out), num_tokens,
                   top_k, hidden, y_rows};
-    return launched(launch(moe_combine_kernel, dim3((num_tokens + 3) / 4), dim3(256), 0, stream, g),
-                    who);
+    const dim3 grid((num_tokens + 3) / 4);
+    hipError_t e;
+    switch (y_rows > 0 ? top_k : 0) {
+        case 1: e = launch(moe_combine_kernel_k<1>, grid, dim3(256), 0, stream, g); break;
+        case 2: e = launch(moe_combine_kernel_k<2>, grid, dim3(256), 0, stream, g); break;
+        case 3: e = launch(moe_combine_kernel_k<3>, grid, dim3(256), 0, stream, g); break;
+        case 4: e = launch(moe_combine_kernel_k<4>, grid, dim3(256), 0, stream, g); break;
+        case 6: e = launch(moe_combine_kernel_k<6>, grid, dim3(256), 0, stream, g); break;
+        case 8: e = launch(moe_combine_kernel_k<8>, grid, dim3(256), 0, stream, g); break;
+        default: e = launch(moe_combine_kernel, grid, dim3(256), 0, stream, g); break;
+    }
+    return launched(e, who);
 }
 
 }  // extern "C"
