@@ -133,6 +133,25 @@ class DeviceArray:
         check(hip().hipMemcpy(out.ctypes.data, self._ptr, self.nbytes, HIP_MEMCPY_D2H), "hipMemcpy D2H")
         return out
 
+    def _span(self, offset: int, nbytes: int) -> int:
+        if offset < 0 or nbytes < 0 or offset + nbytes > self.nbytes:
+            raise ValueError(f"bytes [{offset}, {offset + nbytes}) outside a {self.nbytes}-byte array")
+        return self._ptr + offset
+
+    def upload_at(self, offset: int, arr: np.ndarray) -> None:
+        """Copies arr's bytes to this array at byte `offset` (a slice of a
+        large allocation, e.g. a few blocks of a KV pool)."""
+        arr = np.ascontiguousarray(arr)
+        check(hip().hipMemcpy(self._span(offset, arr.nbytes), arr.ctypes.data, arr.nbytes,
+                              HIP_MEMCPY_H2D), "hipMemcpy H2D")
+
+    def download_at(self, offset: int, shape, dtype) -> np.ndarray:
+        """The bytes at byte `offset` as a host array of shape and dtype."""
+        out = np.empty(shape, dtype=dtype)
+        check(hip().hipMemcpy(out.ctypes.data, self._span(offset, out.nbytes), out.nbytes,
+                              HIP_MEMCPY_D2H), "hipMemcpy D2H")
+        return out
+
     def fill_zero(self) -> None:
         check(hip().hipMemset(self._ptr, 0, self.nbytes), "hipMemset")
 
