@@ -351,6 +351,31 @@ def test_one_long_sequence_many_fragments(dev, G):
         assert_attention_close(dw.run("v2", partition_size=ps), ref, f"long G={G} ps={ps}")
 
 
+@pytest.fixture(scope="module")
+def context_128k(dev):
+    """One sequence of 131,077 tokens (Llama-3's 128k context plus a partial
+    block) beside sequences of 3 and 700, at the 70B head layout (64 query
+    heads, 8 kv heads): 8,244 blocks, 540 MB of K/V. NaN fills the slots
+    past each context in its last block."""
+    rng = np.random.default_rng(128)
+    w = _random_batch(rng, [131_077, 3, 700], H=64, Hkv=8, D=128, extra_blocks=1)
+    for s, L in enumerate(w.context_lens):
+        j = (int(L) - 1) // 16
+        valid = int(L) - 16 * j
+        w.key_cache[w.block_tables[s, j], :, :, valid:] = np.nan
+        w.value_cache[w.block_tables[s, j], :, :, valid:] = np.nan
+    return DeviceWorkload(w), _ref(w)
+
+
+@pytest.mark.parametrize("variant,ps", [("v1", None), ("v2", 512), ("v2", 16), ("v2", 0)])
+def test_context_past_128k(context_128k, variant, ps):
+    """The single pass over 8,193 blocks; split-K with 257 partitions of 512
+    tokens and with 8,193 of 16 (the workgroup reduce's chunked loop many
+    times over, and an 818 MB workspace); balanced mode."""
+    dw, ref = context_128k
+    assert_attention_close(dw.run(variant, partition_size=ps), ref, f"128k {variant} ps={ps}")
+
+
 def test_more_sequences_than_the_lds_tables(dev):
     """4500 short sequences: the single pass drops its longest-first ranking
     (more than 128 sequences), the partition kernel takes one item per
