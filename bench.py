@@ -816,7 +816,8 @@ def bench_prefill(args):
                    "num_heads": H, "num_kv_heads": 8, "head_dim": D, "block_size": 16,
                    "flops_per_call": w.flops(), "algorithmic_bytes_per_call": w.bytes()},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
-                     "frac": round(tflops / 2500.0, 4), "traffic": None},
+                     "frac": round(tflops / 2500.0, 4),
+                     "traffic": read_traffic("prefill_config9_traffic.json")},
         "cpu_baseline": None,
     }
     ceiling = mfma_ceiling(stream, args.no_ceiling)
@@ -865,8 +866,10 @@ def bench_moe_mlp(args):
         "config": {"workload": "mixtral-8x7b-moe-mlp", "num_tokens": T, "hidden": hidden,
                    "intermediate": I, "num_experts": E, "top_k": K, "flops_per_call": flops,
                    "kernels": "rank+route, permute, expert GEMM (gated), expert GEMM, combine"},
+        # traffic: HBM bytes per launch of the dominant kernel, the gated GEMM
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
-                     "frac": round(tflops / 2500.0, 4), "traffic": None},
+                     "frac": round(tflops / 2500.0, 4),
+                     "traffic": read_traffic("moe_mlp_config8_traffic.json")},
         "cpu_baseline": None,
     }
     ceiling = mfma_ceiling(stream, args.no_ceiling)
