@@ -44,6 +44,18 @@ constexpr int kRsrcWord3 = 0x00020000;   // gfx9 buffer resource: raw 32-bit dwo
 typedef __attribute__((address_space(3))) void* lds_ptr;
 __device__ __forceinline__ lds_ptr to_lds(void* p) { return (lds_ptr)p; }
 
+// Waits until at most N of this wave's memory loads are in flight (loads
+// into LDS by buffer_load ... lds are not tracked by the compiler, so their
+// waits are explicit). The empty asm statements keep the compiler from
+// moving LDS reads above it.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt field");
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+    asm volatile("" ::: "memory");
+}
+
 inline bool aligned(const void* p, size_t bytes) {
     return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
 }

@@ -26,7 +26,9 @@
 //   the matrix cores at ~20 TB/s. Tiles are (expert, 256-row tile, column
 //   tile); a workgroup finds its expert from the offsets, and the grid is
 //   sized for the worst case (ceil(rows / 256) + E row tiles); surplus
-//   workgroups exit at once.
+//   workgroups exit at once. An expert's last rows past its whole tiles, when
+//   at most 32, go to a second, HBM-bound kernel instead (thin tiles, below):
+//   a decode batch gives every expert only such rows.
 // combine: out[t, :] = sum_k weights[t, k] * y[inverse[t, k], :] in fp32
 //   (k ascending, fused multiply-add), rounded once to fp16; entries with
 //   inverse outside [0, rows of y) contribute nothing. One wave per token;
@@ -95,6 +97,19 @@ __device__ __forceinline__ f16x mfma32(h8 a, h8 b, f16x c) {
 template <bool GATED>
 constexpr int tile_cols() { return GATED ? kBW / 2 : kBW; }
 
+// An expert's rows past its last whole 256-row tile form its tail. A tail of
+// at most kThinRows rows goes to the thin kernel below instead of a 256-row
+// tile: such a tile costs a whole tile's matrix work and weight staging for a
+// few rows (config 8: 4 of 36 row tiles hold 5 to 31 rows), and a batch of
+// decode tokens gives every expert only such a tail.
+constexpr int kThinRows = 32;
+
+// Row tiles of an expert with `count` rows in the main kernel.
+__device__ __forceinline__ int main_row_tiles(int count) {
+    const int tail = count % kBM;
+    return count / kBM + (tail > kThinRows ? 1 : 0);
+}
+
 template <bool GATED>
 __global__ __launch_bounds__(kThreads) void moe_expert_gemm_kernel(const GemmArgs a) {
     extern __shared__ __align__(16) f16 lds[];
@@ -125,8 +140,7 @@ __global__ __launch_bounds__(kThreads) void moe_expert_gemm_kernel(const GemmArg
         for (int e0 = 0; e0 < a.E; e0 += 64) {
             const int e = e0 + lane;
             int v = 0;
-            if (e < a.E) v = max(a.offsets[e + 1] - a.offsets[e], 0);
-            v = (v + kBM - 1) / kBM;
+            if (e < a.E) v = main_row_tiles(max(a.offsets[e + 1] - a.offsets[e], 0));
             int x = v;
 #pragma unroll
             for (int d = 1; d < 64; d <<= 1) {
@@ -358,6 +372,158 @@ __global__ __launch_bounds__(kThreads) void moe_expert_gemm_kernel(const GemmArg
 }
 
 // ---------------------------------------------------------------------------
+// Thin tiles: the tail of at most kThinRows rows of each expert, times 128
+// output columns per workgroup. A tail this short makes the tile a stream of
+// its weight rows (HBM-bound, 2 * tail FLOP per weight byte), so the kernel
+// is built for bytes in flight: a ring of thin_stages 64-k stages in LDS,
+// each the tile's weight rows and the tail's rows (padded to 32 by repeating
+// the last one), loaded by buffer loads straight into LDS in whole 128-byte
+// lines with the main kernel's chunk swizzle, thin_stages - 1 of them in
+// flight. Four waves of 32 output columns each read their operands from the
+// stage and run v_mfma_f32_32x32x16_f16 with the weight rows as the row
+// operand and the tail rows as the column operand, as in the main kernel, so
+// a lane ends with 4 consecutive output columns of one row. Gated: the
+// stage's first 128 rows are gate rows, the next 128 the matching up rows,
+// two MFMAs per step and the SiLU product in the epilogue.
+// ---------------------------------------------------------------------------
+constexpr int kThinThreads = 256;   // 4 waves
+constexpr int kThinOut = 128;       // output columns per workgroup (32 per wave)
+
+template <bool GATED>
+constexpr int thin_wrows() { return GATED ? 2 * kThinOut : kThinOut; }   // weight rows per stage
+template <bool GATED>
+constexpr int thin_stages() { return GATED ? 4 : 7; }                    // ring depth (<= 160 KiB)
+template <bool GATED>
+constexpr int thin_loads() { return (thin_wrows<GATED>() + kThinRows) * kRowChunks / kThinThreads; }
+template <bool GATED>
+constexpr size_t thin_stage_halfs() { return static_cast<size_t>(thin_wrows<GATED>() + kThinRows) * kBK; }
+template <bool GATED>
+constexpr size_t thin_lds_bytes() { return thin_stages<GATED>() * thin_stage_halfs<GATED>() * sizeof(f16); }
+static_assert(thin_lds_bytes<true>() <= 160 * 1024 && thin_lds_bytes<false>() <= 160 * 1024, "LDS");
+static_assert((kThinRows * kRowChunks) % 64 == 0 && (kThinOut * kRowChunks) % 64 == 0,
+              "each load instruction stays inside one operand");
+
+// Stage ks of a thin tile into LDS buffer buf: load j of wave wv fills chunk
+// slots j * 256 + wv * 64 + lane (8 rows: tile weight rows, then tail rows).
+// A __device__ function rather than a lambda: a lambda issuing these buffer
+// loads made hipcc's host pass drop the kernel's launch stub.
+template <bool GATED>
+__device__ __forceinline__ void thin_issue(f16* lds, __amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t rw,
+                                           __amdgpu_buffer_rsrc_t rw2, const unsigned* off, int wv,
+                                           int ks, int buf) {
+    constexpr int TW = thin_wrows<GATED>();
+    constexpr int L = thin_loads<GATED>();
+    constexpr size_t SH = thin_stage_halfs<GATED>();
+    const unsigned soff = static_cast<unsigned>(ks) * kBK * 2u;
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+        const int r = (j * kThinThreads + wv * 64) / kRowChunks;   // first row of the load
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            r >= TW ? rx : ((GATED && r >= kThinOut) ? rw2 : rw),
+            to_lds(lds + static_cast<size_t>(buf) * SH + (j * kThinThreads + wv * 64) * 8), 16,
+            off[j], soff, 0, 0);
+    }
+}
+
+template <bool GATED>
+__global__ __launch_bounds__(kThinThreads) void moe_expert_thin_kernel(const GemmArgs a) {
+    constexpr int NW = GATED ? 2 : 1;            // weight row tiles per wave
+    constexpr int TW = thin_wrows<GATED>();
+    constexpr int NS = thin_stages<GATED>();
+    constexpr int L = thin_loads<GATED>();       // loads per thread per stage
+    constexpr size_t SH = thin_stage_halfs<GATED>();
+    extern __shared__ __align__(16) f16 lds[];
+    const int e = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int count = max(a.offsets[e + 1] - a.offsets[e], 0);
+    const int tail = count % kBM;
+    if (tail == 0 || tail > kThinRows) return;
+    const int row0 = a.offsets[e] + (count - tail);
+    const int row_end = min(a.offsets[e + 1], a.m_total);
+    if (row0 < 0 || row0 >= row_end) return;
+    const int col0 = blockIdx.x * kThinOut;      // the grid covers n / 128 column tiles
+    const size_t K = static_cast<size_t>(a.k);
+    const unsigned row_bytes = static_cast<unsigned>(K) * 2u;
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<f16*>(a.a + static_cast<size_t>(row0) * K), 0, kThinRows * row_bytes, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<f16*>(a.w + (static_cast<size_t>(e) * a.n + col0) * K), 0, kThinOut * row_bytes,
+        kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rw2 = GATED ? __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<f16*>(a.w2 + (static_cast<size_t>(e) * a.n + col0) * K), 0, kThinOut * row_bytes,
+        kRsrcWord3) : rw;
+    // Byte offset of load j of this lane: stage row r = slot / 8 (weight
+    // rows, then the tail rows), the 8 lanes of a row its 128-byte line.
+    unsigned off[L];
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+        const int sl = j * kThinThreads + wv * 64 + lane;
+        const int r = sl / kRowChunks;
+        const int c = (sl % kRowChunks) ^ ((r >> 1) & (kRowChunks - 1));
+        const int orow = r < TW ? r % kThinOut : min(row0 + (r - TW), row_end - 1) - row0;
+        off[j] = static_cast<unsigned>(orow) * row_bytes + 16u * c;
+    }
+    auto barrier = [] {
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto cslot = [](int r, int c) { return r * kRowChunks + (c ^ ((r >> 1) & (kRowChunks - 1))); };
+    const int lr = lane & 31;
+    const int lc = lane >> 5;
+    f16x acc[NW];
+#pragma unroll
+    for (int i = 0; i < NW; ++i) acc[i] = f16x{};
+
+    const int nk = a.k / kBK;
+    // Stages 0 .. NS - 2 in flight; stages past the last reload the last one
+    // (in bounds, never read as a stage), so every step issues one stage.
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) thin_issue<GATED>(lds, rx, rw, rw2, off, wv, min(s, nk - 1), s);
+    for (int kt = 0; kt < nk; ++kt) {
+        wait_vm<(NS - 2) * L>();   // this wave's loads of stage kt landed
+        barrier();                 // everyone's; and everyone is done with stage kt - 1
+        thin_issue<GATED>(lds, rx, rw, rw2, off, wv, min(kt + NS - 1, nk - 1),
+                          (kt + NS - 1) % NS);   // into stage kt - 1's buffer
+        const f16* st = lds + static_cast<size_t>(kt % NS) * SH;
+#pragma unroll
+        for (int ks = 0; ks < kBK / 16; ++ks) {
+            const int c = 2 * ks + lc;
+            const h8 xf = *reinterpret_cast<const h8*>(st + cslot(TW + lr, c) * 8);
+#pragma unroll
+            for (int i = 0; i < NW; ++i) {
+                const h8 wf = *reinterpret_cast<const h8*>(st + cslot(i * kThinOut + wv * 32 + lr, c) * 8);
+                acc[i] = mfma32(wf, xf, acc[i]);
+            }
+        }
+    }
+    // No load may still be writing this workgroup's LDS when it exits.
+    __builtin_amdgcn_s_waitcnt(0);
+
+    // Lane holds tail row lr and output columns col0 + wv*32 + q*8 + lc*4 + 0..3.
+    const int row = row0 + lr;
+    if (row >= row_end) return;
+    f16* crow = a.c + static_cast<size_t>(row) * a.n + col0 + wv * 32;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        h4 v;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float x = acc[0][q * 4 + r];
+            if constexpr (GATED) {
+                const float u = acc[1][q * 4 + r];
+                x = x / (1.0f + __builtin_amdgcn_exp2f(-x * kLog2e)) * u;
+            }
+            v[r] = static_cast<f16>(x);
+        }
+        *reinterpret_cast<h4*>(crow + q * 8 + lc * 4) = v;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Combine: one wave per token, 8 halfs per lane per step.
 // ---------------------------------------------------------------------------
 struct CombineArgs {
@@ -520,6 +686,17 @@ int swiftllm_hip_moe_expert_gemm(const void* a, const void* w, const void* w2,
                          dim3(kThreads), lds, stream, g)
                 : launch(moe_expert_gemm_kernel<false>, dim3(static_cast<unsigned>(grid)),
                          dim3(kThreads), lds, stream, g);
+    if (err != hipSuccess) return launched(err, who);
+    // The experts' short tails (at most kThinRows rows), which the main grid
+    // leaves out; workgroups of experts without one exit at once.
+    const dim3 thin(static_cast<unsigned>(n / kThinOut), static_cast<unsigned>(num_experts));
+    const size_t tl = gated ? thin_lds_bytes<true>() : thin_lds_bytes<false>();
+    const void* tf = gated ? reinterpret_cast<const void*>(moe_expert_thin_kernel<true>)
+                           : reinterpret_cast<const void*>(moe_expert_thin_kernel<false>);
+    err = hipFuncSetAttribute(tf, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(tl));
+    if (err != hipSuccess) return launched(err, who);
+    err = gated ? launch(moe_expert_thin_kernel<true>, thin, dim3(kThinThreads), tl, stream, g)
+                : launch(moe_expert_thin_kernel<false>, thin, dim3(kThinThreads), tl, stream, g);
     return launched(err, who);
 }
 

@@ -101,16 +101,6 @@ __device__ __forceinline__ void mask_v_pair(int nv0, int nv1, int kg, h8 (&vp)[D
     }
 }
 
-// Waits until at most N of this wave's memory loads are in flight. The
-// empty asm statements keep the compiler from moving LDS reads above it.
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt field");
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
-    asm volatile("" ::: "memory");
-}
-
 // Steps 3 + 4 for one group of 16 query rows over a pair of key blocks (32
 // keys), from the S^T accumulators s0 (first block) and s1 (second): lane
 // (r, kg) holds S^T[t = 4kg + i][g = r] of each. The same online softmax as

@@ -47,6 +47,53 @@ def test_expert_gemm(dev, gated, E, m_total, n, k):
                f"gemm gated={gated} E{E} M{m_total}")
 
 
+@pytest.mark.parametrize("gated,n,k", [(False, 256, 320), (True, 384, 320), (False, 512, 64),
+                                       (True, 128, 128)])
+def test_expert_gemm_thin_tails(dev, gated, n, k):
+    """Expert row counts around the thin-tail limit: tails of at most 32 rows
+    go to the thin kernel, longer ones to a 256-row tile; an expert of 257
+    rows is one whole tile plus a 1-row tail, 288 a whole tile plus a 32-row
+    tail, 289 two tiles. Every output row is checked against the oracle."""
+    counts = [0, 1, 31, 32, 33, 256, 257, 288, 289, 528, 16]
+    rng = np.random.default_rng(n + k + gated)
+    E = len(counts)
+    offs = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    m_total = int(offs[-1])
+    a = (rng.standard_normal((m_total, k)) * 0.5).astype(np.float16)
+    w = (rng.standard_normal((E, n, k)) / np.sqrt(k)).astype(np.float16)
+    w2 = (rng.standard_normal((E, n, k)) / np.sqrt(k)).astype(np.float16) if gated else None
+    c = DeviceArray((m_total, n), np.float16)
+    c.fill_byte(0xFF)
+    moe.moe_expert_gemm(DeviceArray.from_numpy(a), DeviceArray.from_numpy(w),
+                        DeviceArray.from_numpy(w2) if gated else None, DeviceArray.from_numpy(offs), c)
+    synchronize()
+    _close(c.numpy().astype(np.float64), oracle.moe_expert_gemm(a, w, w2, offs),
+           f"thin tails gated={gated} n={n} k={k}")
+
+
+@pytest.mark.parametrize("gated", [False, True])
+def test_expert_gemm_decode_batch(dev, gated):
+    """A decode step's MoE: 64 tokens, top-2 of 8 experts, so every expert
+    holds a few rows and the whole GEMM runs in the thin kernel (k 4096,
+    n 1024)."""
+    rng = np.random.default_rng(64 + gated)
+    E, n, k = 8, 1024, 4096
+    ids = np.stack([rng.choice(E, 2, replace=False) for _ in range(64)])
+    counts = np.bincount(ids.ravel(), minlength=E)
+    offs = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    m_total = int(offs[-1])
+    a = (rng.standard_normal((m_total, k)) * 0.5).astype(np.float16)
+    w = (rng.standard_normal((E, n, k)) / np.sqrt(k)).astype(np.float16)
+    w2 = (rng.standard_normal((E, n, k)) / np.sqrt(k)).astype(np.float16) if gated else None
+    c = DeviceArray((m_total, n), np.float16)
+    c.fill_byte(0xFF)
+    moe.moe_expert_gemm(DeviceArray.from_numpy(a), DeviceArray.from_numpy(w),
+                        DeviceArray.from_numpy(w2) if gated else None, DeviceArray.from_numpy(offs), c)
+    synchronize()
+    _close(c.numpy().astype(np.float64), oracle.moe_expert_gemm(a, w, w2, offs),
+           f"decode batch gated={gated} counts {list(counts)}")
+
+
 @pytest.mark.parametrize("T,K,hidden", [(500, 2, 4096), (300, 1, 4104), (257, 3, 520), (64, 4, 1032),
                                         (33, 5, 4096), (100, 6, 8), (129, 8, 2056), (40, 9, 264)])
 def test_combine(dev, T, K, hidden):
@@ -86,12 +133,23 @@ def test_combine(dev, T, K, hidden):
     assert np.mean(got.view(np.uint16) == ref.view(np.uint16)) > 0.99
 
 
-def test_moe_mlp_chain(dev):
+@pytest.mark.parametrize("T", [96, 1100])
+def test_moe_mlp_chain(dev, T):
     """MoeMlp from router logits: top-2 of 8 experts, hidden 256,
-    intermediate 512, against the oracle chain with the same fp16 rounding
-    of the intermediate activations."""
+    intermediate 512. 96 tokens leave every expert a tail of at most 32 rows
+    (the thin kernel only); 1100 give whole tiles and longer tails as well.
+
+    Each stage is held to the oracle on the GPU's own input to that stage:
+    routing and dispatch bit-exact, the gated GEMM on the permuted rows, the
+    down GEMM on the GPU's fp16 intermediate, the combine on the GPU's expert
+    outputs. Against an oracle chain that rounds its own float64
+    intermediate instead, about 0.1% of the intermediate's elements round to
+    the neighbouring fp16 value, and the down GEMM carries those one-ulp
+    differences into its outputs: that compares two roundings, not the
+    kernels. An indexing mistake in any stage is off by O(rms) in that
+    stage's check."""
     rng = np.random.default_rng(22)
-    T, hidden, I, E, K = 96, 256, 512, 8, 2
+    hidden, I, E, K = 256, 512, 8, 2
     x = rng.standard_normal((T, hidden)).astype(np.float16)
     logits = rng.standard_normal((T, E)).astype(np.float32)
     wg = (rng.standard_normal((E, I, hidden)) / np.sqrt(hidden)).astype(np.float16)
@@ -101,13 +159,21 @@ def test_moe_mlp_chain(dev):
                      DeviceArray.from_numpy(wd))
     out = mlp.forward(DeviceArray.from_numpy(logits), DeviceArray.from_numpy(x))
     synchronize()
+    b = mlp.buffers(T, hidden)
+    d = b["dispatch"]
     ids, w = oracle.moe_route(logits, K)
     counts, offsets, inverse, sorted_ids = oracle.moe_dispatch(ids, E)
-    xp = x[sorted_ids]
-    h = oracle.moe_expert_gemm(xp, wg, wu, offsets).astype(np.float16)
-    y = oracle.moe_expert_gemm(h, wd, None, offsets).astype(np.float16)
-    ref = oracle.moe_combine(y, w.astype(np.float32), inverse)
-    _close(out.numpy().astype(np.float64), ref, "moe mlp")
+    assert np.array_equal(b["ids"].numpy(), ids)
+    assert np.abs(b["weights"].numpy() - w).max() <= 1e-6
+    assert np.array_equal(d.offsets.numpy(), offsets)
+    assert np.array_equal(d.inverse.numpy(), inverse)
+    h = b["h"].numpy()
+    _close(h.astype(np.float64), oracle.moe_expert_gemm(x[sorted_ids], wg, wu, offsets),
+           f"T={T} gated GEMM")
+    y = b["y"].numpy()
+    _close(y.astype(np.float64), oracle.moe_expert_gemm(h, wd, None, offsets), f"T={T} down GEMM")
+    _close(out.numpy().astype(np.float64), oracle.moe_combine(y, b["weights"].numpy(), inverse),
+           f"T={T} combine")
 
 
 def _sample_rows(rng, offs, tile=256, per_tile=2):
