@@ -26,7 +26,8 @@ claim), --config 3 (8 sequences of 32768 tokens, 64 query heads, split-K),
 --config 4 (a ragged step: cache write of 256 new tokens, then decode),
 --config 5 (MoE top-2 routing and dispatch of 4096 tokens, hidden 4096, 8
 experts), and the "next" rows: --config 6/7 (block copies and swaps), 8 (the
-Mixtral MoE layer's expert GEMMs) and 9 (paged prefill).
+Mixtral MoE layer's expert GEMMs), 9 (paged prefill) and 10 (the same MoE
+layer at a 64-token decode batch, where the expert GEMMs stream weights).
 """
 
 from __future__ import annotations
@@ -51,13 +52,14 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", type=int, choices=[1, 2, 3, 4, 5, 6, 7, 8, 9], default=2,
+    ap.add_argument("--config", type=int, choices=[1, 2, 3, 4, 5, 6, 7, 8, 9, 10], default=2,
                     help="1: tiny MHA decode (BASELINE's CPU-runnable case, us only); "
                          "2: Llama-3-8B decode (the metric's workload); 3: long-context split-K; "
                          "4: ragged step (cache write + decode); 5: MoE route + dispatch; "
                          "6: copy_blocks (copy-on-write, 32 layers); 7: swap_blocks out and in; "
                          "8: Mixtral MoE MLP (route, dispatch, expert GEMMs, combine); "
-                         "9: Llama-3-8B paged prefill (8 prompts of 2048 tokens)")
+                         "9: Llama-3-8B paged prefill (8 prompts of 2048 tokens); "
+                         "10: the Mixtral MoE layer at a 64-token decode batch (weights streamed)")
     ap.add_argument("--variant", choices=["v1", "v2"], default=None,
                     help="default: v1 for configs 1 and 2, v2 for configs 3 and 4")
     ap.add_argument("--ceiling", choices=["stream", "gather", "store", "rowcopy", "mfma"], default=None,
@@ -210,6 +212,8 @@ def main():
         return bench_moe_mlp(args)
     if args.config == 9:
         return bench_prefill(args)
+    if args.config == 10:
+        return bench_moe_decode(args)
     if args.rotate is None:
         args.rotate = 4
     if args.variant is None:
@@ -823,6 +827,69 @@ def bench_prefill(args):
     ceiling = mfma_ceiling(stream, args.no_ceiling)
     rec["ceiling"] = ceiling
     rec["ceiling_frac"] = round(tflops / ceiling["value"], 4) if ceiling else None
+    print(json.dumps(rec), flush=True)
+
+
+def bench_moe_decode(args):
+    """Config 10: the Mixtral-8x7B MoE layer of config 8 at a decode batch of
+    64 tokens (top-2 of 8 experts: about 16 rows per expert). Every expert's
+    rows are one short tail, so both expert GEMMs run in the thin kernel and
+    the call streams the gate, up and down weights of every expert that
+    received a token: HBM-bound. Algorithmic bytes per call = those weights +
+    the activations the call reads and writes (x, its permuted copy, the
+    intermediate, the expert outputs, the output); value = those bytes / call
+    time. The live ceiling is the sequential nontemporal read stream."""
+    from swiftllm_amd import moe, workloads
+    from swiftllm_amd._hip import DeviceArray, Stream
+
+    wl = workloads.moe_config(seed=args.seed, num_tokens=64)
+    T, hidden = wl.x.shape
+    E, K, I = wl.num_experts, wl.top_k, 14336
+    rng = np.random.default_rng(args.seed + 1)
+    stream = Stream()
+
+    def stacked(n, k):
+        return DeviceArray.from_numpy(workloads.expert_weights(rng, E, n, k))
+
+    wg, wu, wd = stacked(I, hidden), stacked(I, hidden), stacked(hidden, I)
+    mlp = moe.MoeMlp(E, K, wg, wu, wd)
+    x, logits = DeviceArray.from_numpy(wl.x), DeviceArray.from_numpy(wl.logits)
+
+    def step(i):
+        mlp.forward(logits, x, stream)
+
+    ms, p10, p50, p90 = timed(step, stream, args.steps, args.warmup, min(args.samples, 50))
+    counts = mlp.buffers(T, hidden)["dispatch"].counts.numpy()
+    used = int((counts > 0).sum())
+    rows = T * K
+    weight_bytes = used * 3 * hidden * I * 2
+    act_bytes = 2 * (T * hidden + 2 * rows * hidden + 2 * rows * I + 2 * rows * hidden + T * hidden)
+    alg = weight_bytes + act_bytes
+    value = alg / (ms * 1e-3) / 1e9
+    stream_gbs = None if args.no_ceiling else measure_stream(stream)[0]
+    rec = {
+        "metric": "MoE MLP decode GB/s (expert weights streamed) + us/call @ Mixtral-8x7B layer, 64 tokens",
+        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 6), "us_per_call": round(ms * 1e3, 3),
+        "us_per_call_p10_p50_p90": [round(p10, 2), round(p50, 2), round(p90, 2)],
+        "hbm_peak_frac": round(value / HBM_PEAK_GBS, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f16 in/out, f32 accumulate",
+        "data": "synthetic (seeded normal activations, logits, weights)",
+        "config": {"workload": "mixtral-8x7b-moe-mlp-decode", "num_tokens": T, "hidden": hidden,
+                   "intermediate": I, "num_experts": E, "top_k": K, "experts_used": used,
+                   "rows_per_expert": [int(c) for c in counts],
+                   "algorithmic_bytes_per_call": alg, "weight_bytes_per_call": weight_bytes,
+                   "flops_per_call": 2 * rows * hidden * I * 3,
+                   "kernels": "rank+route, permute, thin expert GEMM (gated), thin expert GEMM, combine"},
+        # traffic: HBM bytes per launch of the dominant kernel, the gated thin GEMM
+        "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4),
+                     "traffic": read_traffic("moe_decode_config10_traffic.json")},
+        "ceiling": {"pattern": "sequential nontemporal read stream (libswiftllm_ceilings)",
+                    "value": round(stream_gbs, 2), "unit": "GB/s"} if stream_gbs else None,
+        "ceiling_frac": round(value / stream_gbs, 4) if stream_gbs else None,
+        "cpu_baseline": None,
+    }
     print(json.dumps(rec), flush=True)
 
 
