@@ -101,8 +101,9 @@ constexpr int tile_cols() { return GATED ? kBW / 2 : kBW; }
 // at most kThinRows rows goes to the thin kernel below instead of a 256-row
 // tile: such a tile costs a whole tile's matrix work and weight staging for a
 // few rows (config 8: 4 of 36 row tiles hold 5 to 31 rows), and a batch of
-// decode tokens gives every expert only such a tail.
-constexpr int kThinRows = 32;
+// decode tokens gives every expert only such a tail (a 256-token batch, top-2
+// of 8 experts: about 64 rows each).
+constexpr int kThinRows = 64;
 
 // Row tiles of an expert with `count` rows in the main kernel.
 __device__ __forceinline__ int main_row_tiles(int count) {
@@ -376,13 +377,15 @@ __global__ __launch_bounds__(kThreads) void moe_expert_gemm_kernel(const GemmArg
 // output columns per workgroup. A tail this short makes the tile a stream of
 // its weight rows (HBM-bound, 2 * tail FLOP per weight byte), so the kernel
 // is built for bytes in flight: a ring of thin_stages 64-k stages in LDS,
-// each the tile's weight rows and the tail's rows (padded to 32 by repeating
+// each the tile's weight rows and the tail's rows (padded to 64 by repeating
 // the last one), loaded by buffer loads straight into LDS in whole 128-byte
 // lines with the main kernel's chunk swizzle, thin_stages - 1 of them in
 // flight. Four waves of 32 output columns each read their operands from the
 // stage and run v_mfma_f32_32x32x16_f16 with the weight rows as the row
-// operand and the tail rows as the column operand, as in the main kernel, so
-// a lane ends with 4 consecutive output columns of one row. Gated: the
+// operand and the tail rows, in two tiles of 32, as the column operand, as in
+// the main kernel, so a lane ends with 4 consecutive output columns of one
+// row per tile. The padding costs MFMA work only: the kernel is bound by
+// streaming the weights. Gated: the
 // stage's first 128 rows are gate rows, the next 128 the matching up rows,
 // two MFMAs per step and the SiLU product in the epilogue.
 // ---------------------------------------------------------------------------
@@ -392,7 +395,7 @@ constexpr int kThinOut = 128;       // output columns per workgroup (32 per wave
 template <bool GATED>
 constexpr int thin_wrows() { return GATED ? 2 * kThinOut : kThinOut; }   // weight rows per stage
 template <bool GATED>
-constexpr int thin_stages() { return GATED ? 4 : 7; }                    // ring depth (<= 160 KiB)
+constexpr int thin_stages() { return GATED ? 4 : 6; }                    // ring depth (<= 160 KiB)
 template <bool GATED>
 constexpr int thin_loads() { return (thin_wrows<GATED>() + kThinRows) * kRowChunks / kThinThreads; }
 template <bool GATED>
@@ -474,9 +477,12 @@ __global__ __launch_bounds__(kThinThreads) void moe_expert_thin_kernel(const Gem
     auto cslot = [](int r, int c) { return r * kRowChunks + (c ^ ((r >> 1) & (kRowChunks - 1))); };
     const int lr = lane & 31;
     const int lc = lane >> 5;
-    f16x acc[NW];
+    constexpr int NT = kThinRows / 32;           // tail row tiles
+    f16x acc[NW][NT];
 #pragma unroll
-    for (int i = 0; i < NW; ++i) acc[i] = f16x{};
+    for (int i = 0; i < NW; ++i)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[i][t] = f16x{};
 
     const int nk = a.k / kBK;
     // Stages 0 .. NS - 2 in flight; stages past the last reload the last one
@@ -492,34 +498,40 @@ __global__ __launch_bounds__(kThinThreads) void moe_expert_thin_kernel(const Gem
 #pragma unroll
         for (int ks = 0; ks < kBK / 16; ++ks) {
             const int c = 2 * ks + lc;
-            const h8 xf = *reinterpret_cast<const h8*>(st + cslot(TW + lr, c) * 8);
+            h8 xf[NT];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) xf[t] = *reinterpret_cast<const h8*>(st + cslot(TW + 32 * t + lr, c) * 8);
 #pragma unroll
             for (int i = 0; i < NW; ++i) {
                 const h8 wf = *reinterpret_cast<const h8*>(st + cslot(i * kThinOut + wv * 32 + lr, c) * 8);
-                acc[i] = mfma32(wf, xf, acc[i]);
+#pragma unroll
+                for (int t = 0; t < NT; ++t) acc[i][t] = mfma32(wf, xf[t], acc[i][t]);
             }
         }
     }
     // No load may still be writing this workgroup's LDS when it exits.
     __builtin_amdgcn_s_waitcnt(0);
 
-    // Lane holds tail row lr and output columns col0 + wv*32 + q*8 + lc*4 + 0..3.
-    const int row = row0 + lr;
-    if (row >= row_end) return;
-    f16* crow = a.c + static_cast<size_t>(row) * a.n + col0 + wv * 32;
+    // Lane holds tail rows 32 t + lr and output columns col0 + wv*32 + q*8 + lc*4 + 0..3.
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        h4 v;
+    for (int t = 0; t < NT; ++t) {
+        const int row = row0 + 32 * t + lr;
+        if (row >= row_end) continue;
+        f16* crow = a.c + static_cast<size_t>(row) * a.n + col0 + wv * 32;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            float x = acc[0][q * 4 + r];
-            if constexpr (GATED) {
-                const float u = acc[1][q * 4 + r];
-                x = x / (1.0f + __builtin_amdgcn_exp2f(-x * kLog2e)) * u;
+        for (int q = 0; q < 4; ++q) {
+            h4 v;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float x = acc[0][t][q * 4 + r];
+                if constexpr (GATED) {
+                    const float u = acc[1][t][q * 4 + r];
+                    x = x / (1.0f + __builtin_amdgcn_exp2f(-x * kLog2e)) * u;
+                }
+                v[r] = static_cast<f16>(x);
             }
-            v[r] = static_cast<f16>(x);
+            *reinterpret_cast<h4*>(crow + q * 8 + lc * 4) = v;
         }
-        *reinterpret_cast<h4*>(crow + q * 8 + lc * 4) = v;
     }
 }
 
