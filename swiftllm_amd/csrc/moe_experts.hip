@@ -674,7 +674,11 @@ int swiftllm_hip_moe_expert_gemm(const void* a, const void* w, const void* w2,
     g.m_total = m_total;
     g.n = n;
     g.k = k;
-    g.m_tiles_max = (m_total + kBM - 1) / kBM + num_experts;
+    // Row tiles of the main grid: whole 256-row tiles hold 256 rows each and
+    // a tail left there holds more than kThinRows, so at most m / 256 of the
+    // first and min(E, m / (kThinRows + 1)) of the second (expert offsets
+    // partition the m_total rows).
+    g.m_tiles_max = m_total / kBM + std::min(num_experts, m_total / (kThinRows + 1));
     g.n_tiles = n / cols;
     g.super_m = (w2 != nullptr) ? kSuperMGated : kSuperMPlain;
     const int super_n = kSuper / g.super_m;
@@ -694,11 +698,13 @@ int swiftllm_hip_moe_expert_gemm(const void* a, const void* w, const void* w2,
     hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                          static_cast<int>(lds));
     if (err != hipSuccess) return launched(err, who);
-    err = gated ? launch(moe_expert_gemm_kernel<true>, dim3(static_cast<unsigned>(grid)),
-                         dim3(kThreads), lds, stream, g)
-                : launch(moe_expert_gemm_kernel<false>, dim3(static_cast<unsigned>(grid)),
-                         dim3(kThreads), lds, stream, g);
-    if (err != hipSuccess) return launched(err, who);
+    if (grid > 0) {  // none when every expert's rows fit one thin tail (m_total <= 64)
+        err = gated ? launch(moe_expert_gemm_kernel<true>, dim3(static_cast<unsigned>(grid)),
+                             dim3(kThreads), lds, stream, g)
+                    : launch(moe_expert_gemm_kernel<false>, dim3(static_cast<unsigned>(grid)),
+                             dim3(kThreads), lds, stream, g);
+        if (err != hipSuccess) return launched(err, who);
+    }
     // The experts' short tails (at most kThinRows rows), which the main grid
     // leaves out; workgroups of experts without one exit at once.
     const dim3 thin(static_cast<unsigned>(n / kThinOut), static_cast<unsigned>(num_experts));

@@ -27,6 +27,7 @@ pytestmark = pytest.mark.gpu
     (8, 1000, 512, 192),
     (1, 257, 256, 64),       # one expert, a 1-row tail tile
     (3, 0, 256, 64),
+    (5, 40, 256, 128),       # 40 rows: no main-grid tile at all, the thin kernel only
 ])
 def test_expert_gemm(dev, gated, E, m_total, n, k):
     """Tiles of 256 rows; columns in tiles of 256 (plain) or 128 (gated)."""
