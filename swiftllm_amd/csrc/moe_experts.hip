@@ -390,12 +390,17 @@ __global__ __launch_bounds__(kThreads) void moe_expert_gemm_kernel(const GemmArg
 // two MFMAs per step and the SiLU product in the epilogue.
 // ---------------------------------------------------------------------------
 constexpr int kThinThreads = 256;   // 4 waves
-constexpr int kThinOut = 128;       // output columns per workgroup (32 per wave)
 
+// Output columns per workgroup: 128 plain (4 waves of 32 columns, each with
+// both 32-row tail tiles), 64 gated (2 column tiles of 32 times the 2 tail
+// tiles, one per wave), so that the gated GEMM's n / 64 x E workgroups of a
+// decode batch (1792 for Mixtral's 14336 x 8) fill whole rounds on 256 CUs.
 template <bool GATED>
-constexpr int thin_wrows() { return GATED ? 2 * kThinOut : kThinOut; }   // weight rows per stage
+constexpr int thin_out() { return GATED ? 64 : 128; }
 template <bool GATED>
-constexpr int thin_stages() { return GATED ? 4 : 6; }                    // ring depth (<= 160 KiB)
+constexpr int thin_wrows() { return GATED ? 2 * thin_out<GATED>() : thin_out<GATED>(); }   // weight rows per stage
+template <bool GATED>
+constexpr int thin_stages() { return 6; }                                // ring depth (<= 160 KiB)
 template <bool GATED>
 constexpr int thin_loads() { return (thin_wrows<GATED>() + kThinRows) * kRowChunks / kThinThreads; }
 template <bool GATED>
@@ -403,7 +408,8 @@ constexpr size_t thin_stage_halfs() { return static_cast<size_t>(thin_wrows<GATE
 template <bool GATED>
 constexpr size_t thin_lds_bytes() { return thin_stages<GATED>() * thin_stage_halfs<GATED>() * sizeof(f16); }
 static_assert(thin_lds_bytes<true>() <= 160 * 1024 && thin_lds_bytes<false>() <= 160 * 1024, "LDS");
-static_assert((kThinRows * kRowChunks) % 64 == 0 && (kThinOut * kRowChunks) % 64 == 0,
+static_assert((kThinRows * kRowChunks) % 64 == 0 && (thin_out<true>() * kRowChunks) % 64 == 0 &&
+                  (thin_out<false>() * kRowChunks) % 64 == 0,
               "each load instruction stays inside one operand");
 
 // Stage ks of a thin tile into LDS buffer buf: load j of wave wv fills chunk
@@ -422,7 +428,7 @@ __device__ __forceinline__ void thin_issue(f16* lds, __amdgpu_buffer_rsrc_t rx, 
     for (int j = 0; j < L; ++j) {
         const int r = (j * kThinThreads + wv * 64) / kRowChunks;   // first row of the load
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            r >= TW ? rx : ((GATED && r >= kThinOut) ? rw2 : rw),
+            r >= TW ? rx : ((GATED && r >= thin_out<GATED>()) ? rw2 : rw),
             to_lds(lds + static_cast<size_t>(buf) * SH + (j * kThinThreads + wv * 64) * 8), 16,
             off[j], soff, 0, 0);
     }
@@ -435,6 +441,9 @@ __global__ __launch_bounds__(kThinThreads) void moe_expert_thin_kernel(const Gem
     constexpr int NS = thin_stages<GATED>();
     constexpr int L = thin_loads<GATED>();       // loads per thread per stage
     constexpr size_t SH = thin_stage_halfs<GATED>();
+    constexpr int OUT = thin_out<GATED>();
+    constexpr int CT = OUT / 32;                 // column tiles per workgroup
+    constexpr int NT = kThinRows / 32 / (4 / CT); // tail tiles per wave
     extern __shared__ __align__(16) f16 lds[];
     const int e = blockIdx.y;
     const int lane = threadIdx.x & 63;
@@ -445,16 +454,18 @@ __global__ __launch_bounds__(kThinThreads) void moe_expert_thin_kernel(const Gem
     const int row0 = a.offsets[e] + (count - tail);
     const int row_end = min(a.offsets[e + 1], a.m_total);
     if (row0 < 0 || row0 >= row_end) return;
-    const int col0 = blockIdx.x * kThinOut;      // the grid covers n / 128 column tiles
+    const int col0 = blockIdx.x * OUT;           // the grid covers n / OUT column tiles
+    const int ct = wv % CT;                      // this wave's column tile
+    const int t0 = (wv / CT) * NT;               // and its first tail tile
     const size_t K = static_cast<size_t>(a.k);
     const unsigned row_bytes = static_cast<unsigned>(K) * 2u;
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<f16*>(a.a + static_cast<size_t>(row0) * K), 0, kThinRows * row_bytes, kRsrcWord3);
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<f16*>(a.w + (static_cast<size_t>(e) * a.n + col0) * K), 0, kThinOut * row_bytes,
+        const_cast<f16*>(a.w + (static_cast<size_t>(e) * a.n + col0) * K), 0, OUT * row_bytes,
         kRsrcWord3);
     const __amdgpu_buffer_rsrc_t rw2 = GATED ? __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<f16*>(a.w2 + (static_cast<size_t>(e) * a.n + col0) * K), 0, kThinOut * row_bytes,
+        const_cast<f16*>(a.w2 + (static_cast<size_t>(e) * a.n + col0) * K), 0, OUT * row_bytes,
         kRsrcWord3) : rw;
     // Byte offset of load j of this lane: stage row r = slot / 8 (weight
     // rows, then the tail rows), the 8 lanes of a row its 128-byte line.
@@ -464,7 +475,7 @@ __global__ __launch_bounds__(kThinThreads) void moe_expert_thin_kernel(const Gem
         const int sl = j * kThinThreads + wv * 64 + lane;
         const int r = sl / kRowChunks;
         const int c = (sl % kRowChunks) ^ ((r >> 1) & (kRowChunks - 1));
-        const int orow = r < TW ? r % kThinOut : min(row0 + (r - TW), row_end - 1) - row0;
+        const int orow = r < TW ? r % OUT : min(row0 + (r - TW), row_end - 1) - row0;
         off[j] = static_cast<unsigned>(orow) * row_bytes + 16u * c;
     }
     auto barrier = [] {
@@ -477,7 +488,6 @@ __global__ __launch_bounds__(kThinThreads) void moe_expert_thin_kernel(const Gem
     auto cslot = [](int r, int c) { return r * kRowChunks + (c ^ ((r >> 1) & (kRowChunks - 1))); };
     const int lr = lane & 31;
     const int lc = lane >> 5;
-    constexpr int NT = kThinRows / 32;           // tail row tiles
     f16x acc[NW][NT];
 #pragma unroll
     for (int i = 0; i < NW; ++i)
@@ -500,10 +510,10 @@ __global__ __launch_bounds__(kThinThreads) void moe_expert_thin_kernel(const Gem
             const int c = 2 * ks + lc;
             h8 xf[NT];
 #pragma unroll
-            for (int t = 0; t < NT; ++t) xf[t] = *reinterpret_cast<const h8*>(st + cslot(TW + 32 * t + lr, c) * 8);
+            for (int t = 0; t < NT; ++t) xf[t] = *reinterpret_cast<const h8*>(st + cslot(TW + 32 * (t0 + t) + lr, c) * 8);
 #pragma unroll
             for (int i = 0; i < NW; ++i) {
-                const h8 wf = *reinterpret_cast<const h8*>(st + cslot(i * kThinOut + wv * 32 + lr, c) * 8);
+                const h8 wf = *reinterpret_cast<const h8*>(st + cslot(i * OUT + ct * 32 + lr, c) * 8);
 #pragma unroll
                 for (int t = 0; t < NT; ++t) acc[i][t] = mfma32(wf, xf[t], acc[i][t]);
             }
@@ -512,12 +522,12 @@ __global__ __launch_bounds__(kThinThreads) void moe_expert_thin_kernel(const Gem
     // No load may still be writing this workgroup's LDS when it exits.
     __builtin_amdgcn_s_waitcnt(0);
 
-    // Lane holds tail rows 32 t + lr and output columns col0 + wv*32 + q*8 + lc*4 + 0..3.
+    // Lane holds tail rows 32 (t0 + t) + lr and output columns col0 + ct*32 + q*8 + lc*4 + 0..3.
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-        const int row = row0 + 32 * t + lr;
+        const int row = row0 + 32 * (t0 + t) + lr;
         if (row >= row_end) continue;
-        f16* crow = a.c + static_cast<size_t>(row) * a.n + col0 + wv * 32;
+        f16* crow = a.c + static_cast<size_t>(row) * a.n + col0 + ct * 32;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             h4 v;
@@ -707,7 +717,8 @@ int swiftllm_hip_moe_expert_gemm(const void* a, const void* w, const void* w2,
     }
     // The experts' short tails (at most kThinRows rows), which the main grid
     // leaves out; workgroups of experts without one exit at once.
-    const dim3 thin(static_cast<unsigned>(n / kThinOut), static_cast<unsigned>(num_experts));
+    const dim3 thin(static_cast<unsigned>(n / (gated ? thin_out<true>() : thin_out<false>())),
+                    static_cast<unsigned>(num_experts));
     const size_t tl = gated ? thin_lds_bytes<true>() : thin_lds_bytes<false>();
     const void* tf = gated ? reinterpret_cast<const void*>(moe_expert_thin_kernel<true>)
                            : reinterpret_cast<const void*>(moe_expert_thin_kernel<false>);
