@@ -25,10 +25,11 @@
 //   and up value of each of its columns. The 256 x 256 tile does 128 FLOP per byte staged, so L2 feeds
 //   the matrix cores at ~20 TB/s. Tiles are (expert, 256-row tile, column
 //   tile); a workgroup finds its expert from the offsets, and the grid is
-//   sized for the worst case (ceil(rows / 256) + E row tiles); surplus
-//   workgroups exit at once. An expert's last rows past its whole tiles, when
-//   at most 32, go to a second, HBM-bound kernel instead (thin tiles, below):
-//   a decode batch gives every expert only such rows.
+//   sized for the worst case (rows / 256 whole tiles plus min(E, rows / 65)
+//   tails of more than 64 rows); surplus workgroups exit at once. An
+//   expert's last rows past its whole tiles, when at most 64, go to a second,
+//   HBM-bound kernel instead (thin tiles, below): a decode batch gives every
+//   expert only such rows.
 // combine: out[t, :] = sum_k weights[t, k] * y[inverse[t, k], :] in fp32
 //   (k ascending, fused multiply-add), rounded once to fp16; entries with
 //   inverse outside [0, rows of y) contribute nothing. One wave per token;
@@ -373,21 +374,21 @@ __global__ __launch_bounds__(kThreads) void moe_expert_gemm_kernel(const GemmArg
 }
 
 // ---------------------------------------------------------------------------
-// Thin tiles: the tail of at most kThinRows rows of each expert, times 128
-// output columns per workgroup. A tail this short makes the tile a stream of
-// its weight rows (HBM-bound, 2 * tail FLOP per weight byte), so the kernel
-// is built for bytes in flight: a ring of thin_stages 64-k stages in LDS,
-// each the tile's weight rows and the tail's rows (padded to 64 by repeating
-// the last one), loaded by buffer loads straight into LDS in whole 128-byte
-// lines with the main kernel's chunk swizzle, thin_stages - 1 of them in
-// flight. Four waves of 32 output columns each read their operands from the
-// stage and run v_mfma_f32_32x32x16_f16 with the weight rows as the row
-// operand and the tail rows, in two tiles of 32, as the column operand, as in
-// the main kernel, so a lane ends with 4 consecutive output columns of one
-// row per tile. The padding costs MFMA work only: the kernel is bound by
-// streaming the weights. Gated: the
-// stage's first 128 rows are gate rows, the next 128 the matching up rows,
-// two MFMAs per step and the SiLU product in the epilogue.
+// Thin tiles: the tail of at most kThinRows rows of each expert, times
+// thin_out output columns per workgroup. A tail this short makes the tile a
+// stream of its weight rows (HBM-bound, 2 * tail FLOP per weight byte), so the
+// kernel is built for bytes in flight: a ring of thin_stages 64-k stages in
+// LDS, each the tile's weight rows and the tail's rows (padded to 64 by
+// repeating the last one), loaded by buffer loads straight into LDS in whole
+// 128-byte lines with the main kernel's chunk swizzle, thin_stages - 1 of
+// them in flight. The four waves read their operands from the stage and run
+// v_mfma_f32_32x32x16_f16 with 32 weight rows as the row operand and 32 tail
+// rows as the column operand, as in the main kernel, so a lane ends with 4
+// consecutive output columns of one row per tail tile. The padding costs MFMA
+// work only: the kernel is bound by streaming the weights. Gated: the stage's
+// first thin_out weight rows are gate rows, the next thin_out the matching up
+// rows; a wave multiplies both for its columns and forms the SiLU product in
+// the epilogue.
 // ---------------------------------------------------------------------------
 constexpr int kThinThreads = 256;   // 4 waves
 

@@ -138,7 +138,7 @@ def test_combine(dev, T, K, hidden):
 @pytest.mark.parametrize("T", [96, 1100])
 def test_moe_mlp_chain(dev, T):
     """MoeMlp from router logits: top-2 of 8 experts, hidden 256,
-    intermediate 512. 96 tokens leave every expert a tail of at most 32 rows
+    intermediate 512. 96 tokens leave every expert a tail of at most 64 rows
     (the thin kernel only); 1100 give whole tiles and longer tails as well.
 
     Each stage is held to the oracle on the GPU's own input to that stage:
