@@ -1,6 +1,7 @@
 """The hot path inside a HIP graph: a ragged decode step (cache write, then
-single-pass and balanced decode) and the fused MoE route + dispatch are
-captured once and replayed several times, with new inputs uploaded and the
+single-pass and balanced decode), the fused MoE route + dispatch, and the
+whole MoE layer (MoeMlp.forward: dispatch, expert GEMMs with their thin
+tails, combine) are captured once and replayed several times, with new inputs uploaded and the
 program's own eager work and synchronisation between replays; every replay
 must equal the eager run on the same inputs bit for bit (the kernels are
 deterministic), and the decode outputs also meet the attention tolerance."""
@@ -109,3 +110,43 @@ def test_moe_route_dispatch_graph_replays_match_eager(dev):
         assert np.array_equal(bufs.offsets.numpy(), offsets)
         assert np.array_equal(bufs.inverse.numpy(), inverse)
         assert np.array_equal(bufs.x_perm.numpy().view(np.uint16), xx[sorted_ids].view(np.uint16))
+
+
+def test_moe_mlp_graph_replays_match_eager(dev):
+    """MoeMlp.forward whole: route + dispatch, the gated and the down expert
+    GEMM (main grid and thin tails: 1100 tokens give every expert a whole
+    256-row tile and a short tail) and the combine, captured once; each of
+    three replays on new router logits and activations equals the eager
+    forward on the same inputs bit for bit."""
+    rng = np.random.default_rng(35)
+    T, hidden, I, E, K = 1100, 256, 512, 8, 2
+    wg = (rng.standard_normal((E, I, hidden)) / np.sqrt(hidden)).astype(np.float16)
+    wu = (rng.standard_normal((E, I, hidden)) / np.sqrt(hidden)).astype(np.float16)
+    wd = (rng.standard_normal((E, hidden, I)) / np.sqrt(I)).astype(np.float16)
+    mlp = moe.MoeMlp(E, K, DeviceArray.from_numpy(wg), DeviceArray.from_numpy(wu),
+                     DeviceArray.from_numpy(wd))
+    logits = DeviceArray((T, E), np.float32)
+    x = DeviceArray((T, hidden), np.float16)
+    logits.upload(rng.standard_normal((T, E)).astype(np.float32))
+    x.upload(rng.standard_normal((T, hidden)).astype(np.float16))
+    stream = Stream()
+    mlp.forward(logits, x, stream)   # buffers exist before the capture
+    stream.synchronize()
+    out = {}
+    graph = Graph(stream, lambda: out.setdefault("dev", mlp.forward(logits, x, stream)))
+    tails = []
+    for rep in range(3):
+        logits.upload(rng.standard_normal((T, E)).astype(np.float32))
+        x.upload(rng.standard_normal((T, hidden)).astype(np.float16))
+        synchronize()
+        eager = mlp.forward(logits, x, stream)
+        stream.synchronize()
+        ref = eager.numpy()
+        counts = mlp.buffers(T, hidden)["dispatch"].counts.numpy()
+        tails.append(int(((counts % 256 > 0) & (counts % 256 <= 64)).sum()))
+        out["dev"].fill_byte(0xFF)
+        synchronize()
+        graph.launch(stream)
+        stream.synchronize()
+        assert np.array_equal(out["dev"].numpy().view(np.uint16), ref.view(np.uint16)), rep
+    assert min(tails) > 0, "every replay must include thin tails"
