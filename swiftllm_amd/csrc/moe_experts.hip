@@ -25,9 +25,9 @@
 //   and up value of each of its columns. The 256 x 256 tile does 128 FLOP per byte staged, so L2 feeds
 //   the matrix cores at ~20 TB/s. Tiles are (expert, 256-row tile, column
 //   tile); a workgroup finds its expert from the offsets, and the grid is
-//   sized for the worst case (rows / 256 whole tiles plus min(E, rows / 65)
-//   tails of more than 64 rows); surplus workgroups exit at once. An
-//   expert's last rows past its whole tiles, when at most 64, go to a second,
+//   sized for the worst case (rows / 256 whole tiles plus min(E, rows / 129)
+//   tails of more than 128 rows); surplus workgroups exit at once. An
+//   expert's last rows past its whole tiles, when at most 128, go to a second,
 //   HBM-bound kernel instead (thin tiles, below): a decode batch gives every
 //   expert only such rows.
 // combine: out[t, :] = sum_k weights[t, k] * y[inverse[t, k], :] in fp32
@@ -102,9 +102,9 @@ constexpr int tile_cols() { return GATED ? kBW / 2 : kBW; }
 // at most kThinRows rows goes to the thin kernel below instead of a 256-row
 // tile: such a tile costs a whole tile's matrix work and weight staging for a
 // few rows (config 8: 4 of 36 row tiles hold 5 to 31 rows), and a batch of
-// decode tokens gives every expert only such a tail (a 256-token batch, top-2
-// of 8 experts: about 64 rows each).
-constexpr int kThinRows = 64;
+// decode tokens gives every expert only such a tail (a 512-token batch, top-2
+// of 8 experts: about 128 rows each).
+constexpr int kThinRows = 128;
 
 // Row tiles of an expert with `count` rows in the main kernel.
 __device__ __forceinline__ int main_row_tiles(int count) {
@@ -378,115 +378,100 @@ __global__ __launch_bounds__(kThreads) void moe_expert_gemm_kernel(const GemmArg
 // thin_out output columns per workgroup. A tail this short makes the tile a
 // stream of its weight rows (HBM-bound, 2 * tail FLOP per weight byte), so the
 // kernel is built for bytes in flight: a ring of thin_stages 64-k stages in
-// LDS, each the tile's weight rows and the tail's rows (padded to 64 by
+// LDS, each the tile's weight rows and the tail's rows (padded to 128 by
 // repeating the last one), loaded by buffer loads straight into LDS in whole
 // 128-byte lines with the main kernel's chunk swizzle, thin_stages - 1 of
 // them in flight. The four waves read their operands from the stage and run
 // v_mfma_f32_32x32x16_f16 with 32 weight rows as the row operand and 32 tail
 // rows as the column operand, as in the main kernel, so a lane ends with 4
-// consecutive output columns of one row per tail tile. The padding costs MFMA
-// work only: the kernel is bound by streaming the weights. Gated: the stage's
+// consecutive output columns of one row per tail tile. The padding rows cost
+// MFMA work and L2 hits only: the kernel is bound by streaming the weights. Gated: the stage's
 // first thin_out weight rows are gate rows, the next thin_out the matching up
 // rows; a wave multiplies both for its columns and forms the SiLU product in
 // the epilogue.
 // ---------------------------------------------------------------------------
 constexpr int kThinThreads = 256;   // 4 waves
+constexpr int kThinLds = 160 * 1024;
 
-// Output columns per workgroup: 128 plain (4 waves of 32 columns, each with
-// both 32-row tail tiles), 64 gated (2 column tiles of 32 times the 2 tail
-// tiles, one per wave), so that the gated GEMM's n / 64 x E workgroups of a
-// decode batch (1792 for Mixtral's 14336 x 8) fill whole rounds on 256 CUs.
+// Output columns per workgroup: 128 plain (4 waves of 32 columns), 64 gated
+// (2 column tiles of 32, each for two waves that share its tail tiles), so
+// that the gated GEMM's n / 64 x E workgroups of a decode batch (1792 for
+// Mixtral's 14336 x 8) fill whole rounds on 256 CUs.
 template <bool GATED>
 constexpr int thin_out() { return GATED ? 64 : 128; }
-template <bool GATED>
-constexpr int thin_wrows() { return GATED ? 2 * thin_out<GATED>() : thin_out<GATED>(); }   // weight rows per stage
-template <bool GATED>
-constexpr int thin_stages() { return 6; }                                // ring depth (<= 160 KiB)
-template <bool GATED>
-constexpr int thin_loads() { return (thin_wrows<GATED>() + kThinRows) * kRowChunks / kThinThreads; }
-template <bool GATED>
-constexpr size_t thin_stage_halfs() { return static_cast<size_t>(thin_wrows<GATED>() + kThinRows) * kBK; }
-template <bool GATED>
-constexpr size_t thin_lds_bytes() { return thin_stages<GATED>() * thin_stage_halfs<GATED>() * sizeof(f16); }
-static_assert(thin_lds_bytes<true>() <= 160 * 1024 && thin_lds_bytes<false>() <= 160 * 1024, "LDS");
-static_assert((kThinRows * kRowChunks) % 64 == 0 && (thin_out<true>() * kRowChunks) % 64 == 0 &&
-                  (thin_out<false>() * kRowChunks) % 64 == 0,
-              "each load instruction stays inside one operand");
+
+// A thin tile's shape for a tail of at most 32 NTT rows (NTT = 1, 2 or 4
+// tiles of 32): a stage holds the tile's TW weight rows and 32 NTT tail rows
+// (the last one repeated), and as many stages as fit in the LDS make the
+// ring (8 for NTT = 1, 6 for 2, 5 for 4), so short tails, which load fewer
+// rows per stage, keep more stages in flight.
+template <bool GATED, int NTT>
+struct Thin {
+    static constexpr int OUT = thin_out<GATED>();
+    static constexpr int TW = GATED ? 2 * OUT : OUT;              // weight rows per stage
+    static constexpr int ROWS = TW + 32 * NTT;                     // stage rows
+    static constexpr int L = ROWS * kRowChunks / kThinThreads;    // loads per thread per stage
+    static constexpr size_t SH = static_cast<size_t>(ROWS) * kBK; // stage size in halves
+    static constexpr int NS = kThinLds / static_cast<int>(SH * sizeof(f16));
+    static constexpr int CT = OUT / 32;                           // column tiles
+    static constexpr int NT = (NTT * CT + 3) / 4;                 // tail tiles per wave
+    static_assert(ROWS * kRowChunks % kThinThreads == 0 && (TW * kRowChunks) % 64 == 0 &&
+                      (OUT * kRowChunks) % 64 == 0,
+                  "each load instruction stays inside one operand");
+    static_assert(NS >= 3 && (NS - 2) * L < 64, "ring and vmcnt field");
+};
 
 // Stage ks of a thin tile into LDS buffer buf: load j of wave wv fills chunk
 // slots j * 256 + wv * 64 + lane (8 rows: tile weight rows, then tail rows).
 // A __device__ function rather than a lambda: a lambda issuing these buffer
 // loads made hipcc's host pass drop the kernel's launch stub.
-template <bool GATED>
+template <bool GATED, int NTT>
 __device__ __forceinline__ void thin_issue(f16* lds, __amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t rw,
                                            __amdgpu_buffer_rsrc_t rw2, const unsigned* off, int wv,
                                            int ks, int buf) {
-    constexpr int TW = thin_wrows<GATED>();
-    constexpr int L = thin_loads<GATED>();
-    constexpr size_t SH = thin_stage_halfs<GATED>();
+    using C = Thin<GATED, NTT>;
     const unsigned soff = static_cast<unsigned>(ks) * kBK * 2u;
 #pragma unroll
-    for (int j = 0; j < L; ++j) {
+    for (int j = 0; j < C::L; ++j) {
         const int r = (j * kThinThreads + wv * 64) / kRowChunks;   // first row of the load
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            r >= TW ? rx : ((GATED && r >= thin_out<GATED>()) ? rw2 : rw),
-            to_lds(lds + static_cast<size_t>(buf) * SH + (j * kThinThreads + wv * 64) * 8), 16,
+            r >= C::TW ? rx : ((GATED && r >= C::OUT) ? rw2 : rw),
+            to_lds(lds + static_cast<size_t>(buf) * C::SH + (j * kThinThreads + wv * 64) * 8), 16,
             off[j], soff, 0, 0);
     }
 }
 
-template <bool GATED>
-__global__ __launch_bounds__(kThinThreads) void moe_expert_thin_kernel(const GemmArgs a) {
+// One thin tile: expert e's tail rows [row0, row_end) (tail = their count)
+// times output columns [col0, col0 + OUT).
+template <bool GATED, int NTT>
+__device__ __forceinline__ void thin_tile(const GemmArgs& a, f16* lds, int e, int row0, int row_end,
+                                          int tail, int col0, int wv, int lane) {
+    using C = Thin<GATED, NTT>;
     constexpr int NW = GATED ? 2 : 1;            // weight row tiles per wave
-    constexpr int TW = thin_wrows<GATED>();
-    constexpr int NS = thin_stages<GATED>();
-    constexpr int L = thin_loads<GATED>();       // loads per thread per stage
-    constexpr size_t SH = thin_stage_halfs<GATED>();
-    constexpr int OUT = thin_out<GATED>();
-    constexpr int CT = OUT / 32;                 // column tiles per workgroup
-    constexpr int NT = kThinRows / 32 / (4 / CT); // tail tiles per wave
-    extern __shared__ __align__(16) f16 lds[];
-    const int e = blockIdx.y;
-    const int lane = threadIdx.x & 63;
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int count = max(a.offsets[e + 1] - a.offsets[e], 0);
-    const int tail = count % kBM;
-    if (tail == 0 || tail > kThinRows) return;
-    const int row0 = a.offsets[e] + (count - tail);
-    const int row_end = min(a.offsets[e + 1], a.m_total);
-    if (row0 < 0 || row0 >= row_end) return;
-    const int col0 = blockIdx.x * OUT;           // the grid covers n / OUT column tiles
-    const int ct = wv % CT;                      // this wave's column tile
-    const int t0 = (wv / CT) * NT;               // and its first tail tile
+    constexpr int NT = C::NT;
+    const int ct = wv % C::CT;                   // this wave's column tile
+    const int t0 = (wv / C::CT) * NT;            // and its first tail tile
     const size_t K = static_cast<size_t>(a.k);
     const unsigned row_bytes = static_cast<unsigned>(K) * 2u;
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<f16*>(a.a + static_cast<size_t>(row0) * K), 0, kThinRows * row_bytes, kRsrcWord3);
+        const_cast<f16*>(a.a + static_cast<size_t>(row0) * K), 0, 32 * NTT * row_bytes, kRsrcWord3);
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<f16*>(a.w + (static_cast<size_t>(e) * a.n + col0) * K), 0, OUT * row_bytes,
+        const_cast<f16*>(a.w + (static_cast<size_t>(e) * a.n + col0) * K), 0, C::OUT * row_bytes,
         kRsrcWord3);
     const __amdgpu_buffer_rsrc_t rw2 = GATED ? __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<f16*>(a.w2 + (static_cast<size_t>(e) * a.n + col0) * K), 0, OUT * row_bytes,
+        const_cast<f16*>(a.w2 + (static_cast<size_t>(e) * a.n + col0) * K), 0, C::OUT * row_bytes,
         kRsrcWord3) : rw;
     // Byte offset of load j of this lane: stage row r = slot / 8 (weight
     // rows, then the tail rows), the 8 lanes of a row its 128-byte line.
-    unsigned off[L];
+    unsigned off[C::L];
 #pragma unroll
-    for (int j = 0; j < L; ++j) {
+    for (int j = 0; j < C::L; ++j) {
         const int sl = j * kThinThreads + wv * 64 + lane;
         const int r = sl / kRowChunks;
         const int c = (sl % kRowChunks) ^ ((r >> 1) & (kRowChunks - 1));
-        const int orow = r < TW ? r % OUT : min(row0 + (r - TW), row_end - 1) - row0;
+        const int orow = r < C::TW ? r % C::OUT : min(row0 + (r - C::TW), row_end - 1) - row0;
         off[j] = static_cast<unsigned>(orow) * row_bytes + 16u * c;
     }
-    auto barrier = [] {
-        __builtin_amdgcn_sched_barrier(0);
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    auto cslot = [](int r, int c) { return r * kRowChunks + (c ^ ((r >> 1) & (kRowChunks - 1))); };
     const int lr = lane & 31;
     const int lc = lane >> 5;
     f16x acc[NW][NT];
@@ -496,25 +481,40 @@ __global__ __launch_bounds__(kThinThreads) void moe_expert_thin_kernel(const Gem
         for (int t = 0; t < NT; ++t) acc[i][t] = f16x{};
 
     const int nk = a.k / kBK;
+    constexpr int NS = C::NS;
     // Stages 0 .. NS - 2 in flight; stages past the last reload the last one
     // (in bounds, never read as a stage), so every step issues one stage.
 #pragma unroll
-    for (int s = 0; s < NS - 1; ++s) thin_issue<GATED>(lds, rx, rw, rw2, off, wv, min(s, nk - 1), s);
+    for (int s = 0; s < NS - 1; ++s) thin_issue<GATED, NTT>(lds, rx, rw, rw2, off, wv, min(s, nk - 1), s);
     for (int kt = 0; kt < nk; ++kt) {
-        wait_vm<(NS - 2) * L>();   // this wave's loads of stage kt landed
-        barrier();                 // everyone's; and everyone is done with stage kt - 1
-        thin_issue<GATED>(lds, rx, rw, rw2, off, wv, min(kt + NS - 1, nk - 1),
-                          (kt + NS - 1) % NS);   // into stage kt - 1's buffer
-        const f16* st = lds + static_cast<size_t>(kt % NS) * SH;
+        wait_vm<(NS - 2) * C::L>();   // this wave's loads of stage kt landed
+        // Everyone's, and everyone is done with stage kt - 1. The empty asm
+        // statements keep the compiler from moving memory operations across.
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        thin_issue<GATED, NTT>(lds, rx, rw, rw2, off, wv, min(kt + NS - 1, nk - 1),
+                               (kt + NS - 1) % NS);   // into stage kt - 1's buffer
+        const f16* st = lds + static_cast<size_t>(kt % NS) * C::SH;
 #pragma unroll
         for (int ks = 0; ks < kBK / 16; ++ks) {
             const int c = 2 * ks + lc;
             h8 xf[NT];
 #pragma unroll
-            for (int t = 0; t < NT; ++t) xf[t] = *reinterpret_cast<const h8*>(st + cslot(TW + 32 * (t0 + t) + lr, c) * 8);
+            for (int t = 0; t < NT; ++t) {
+                const int r = C::TW + 32 * min(t0 + t, NTT - 1) + lr;
+                xf[t] = *reinterpret_cast<const h8*>(st + (r * kRowChunks + (c ^ ((r >> 1) & (kRowChunks - 1)))) * 8);
+            }
 #pragma unroll
             for (int i = 0; i < NW; ++i) {
-                const h8 wf = *reinterpret_cast<const h8*>(st + cslot(i * OUT + ct * 32 + lr, c) * 8);
+                const int r = i * C::OUT + ct * 32 + lr;
+                const h8 wf = *reinterpret_cast<const h8*>(st + (r * kRowChunks + (c ^ ((r >> 1) & (kRowChunks - 1)))) * 8);
+                // Every tile unconditionally: a branch per MFMA made the
+                // allocator copy the accumulators between AGPRs and VGPRs
+                // around each one (2x slower gated). Padding rows repeat the
+                // last tail row, so their results are finite and not stored.
 #pragma unroll
                 for (int t = 0; t < NT; ++t) acc[i][t] = mfma32(wf, xf[t], acc[i][t]);
             }
@@ -527,7 +527,7 @@ __global__ __launch_bounds__(kThinThreads) void moe_expert_thin_kernel(const Gem
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const int row = row0 + 32 * (t0 + t) + lr;
-        if (row >= row_end) continue;
+        if (t0 + t >= NTT || row >= row_end) continue;
         f16* crow = a.c + static_cast<size_t>(row) * a.n + col0 + ct * 32;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -544,6 +544,25 @@ __global__ __launch_bounds__(kThinThreads) void moe_expert_thin_kernel(const Gem
             *reinterpret_cast<h4*>(crow + q * 8 + lc * 4) = v;
         }
     }
+}
+
+template <bool GATED>
+__global__ __launch_bounds__(kThinThreads) void moe_expert_thin_kernel(const GemmArgs a) {
+    extern __shared__ __align__(16) f16 lds[];
+    const int e = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int count = max(a.offsets[e + 1] - a.offsets[e], 0);
+    const int tail = count % kBM;
+    if (tail == 0 || tail > kThinRows) return;
+    const int row0 = a.offsets[e] + (count - tail);
+    const int row_end = min(a.offsets[e + 1], a.m_total);
+    if (row0 < 0 || row0 >= row_end) return;
+    const int col0 = blockIdx.x * thin_out<GATED>();   // the grid covers n / OUT column tiles
+    // Uniform over the workgroup: the tile shape for this tail.
+    if (tail <= 32) thin_tile<GATED, 1>(a, lds, e, row0, row_end, tail, col0, wv, lane);
+    else if (tail <= 64) thin_tile<GATED, 2>(a, lds, e, row0, row_end, tail, col0, wv, lane);
+    else thin_tile<GATED, 4>(a, lds, e, row0, row_end, tail, col0, wv, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -709,7 +728,7 @@ int swiftllm_hip_moe_expert_gemm(const void* a, const void* w, const void* w2,
     hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                          static_cast<int>(lds));
     if (err != hipSuccess) return launched(err, who);
-    if (grid > 0) {  // none when every expert's rows fit one thin tail (m_total <= 64)
+    if (grid > 0) {  // none when every expert's rows fit one thin tail (m_total <= 128)
         err = gated ? launch(moe_expert_gemm_kernel<true>, dim3(static_cast<unsigned>(grid)),
                              dim3(kThreads), lds, stream, g)
                     : launch(moe_expert_gemm_kernel<false>, dim3(static_cast<unsigned>(grid)),
@@ -720,7 +739,7 @@ int swiftllm_hip_moe_expert_gemm(const void* a, const void* w, const void* w2,
     // leaves out; workgroups of experts without one exit at once.
     const dim3 thin(static_cast<unsigned>(n / (gated ? thin_out<true>() : thin_out<false>())),
                     static_cast<unsigned>(num_experts));
-    const size_t tl = gated ? thin_lds_bytes<true>() : thin_lds_bytes<false>();
+    const size_t tl = kThinLds;
     const void* tf = gated ? reinterpret_cast<const void*>(moe_expert_thin_kernel<true>)
                            : reinterpret_cast<const void*>(moe_expert_thin_kernel<false>);
     err = hipFuncSetAttribute(tf, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(tl));

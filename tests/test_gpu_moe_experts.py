@@ -51,12 +51,12 @@ def test_expert_gemm(dev, gated, E, m_total, n, k):
 @pytest.mark.parametrize("gated,n,k", [(False, 256, 320), (True, 384, 320), (False, 512, 64),
                                        (True, 128, 128)])
 def test_expert_gemm_thin_tails(dev, gated, n, k):
-    """Expert row counts around the thin-tail limit: tails of at most 64 rows
-    go to the thin kernel (two 32-row tiles), longer ones to a 256-row tile;
-    an expert of 257 rows is one whole tile plus a 1-row tail, 320 a whole
-    tile plus a 64-row tail, 321 two tiles. Every output row is checked
-    against the oracle."""
-    counts = [0, 1, 31, 32, 33, 64, 65, 256, 257, 288, 320, 321, 528, 16]
+    """Expert row counts around the thin-tail limit: tails of at most 128 rows
+    go to the thin kernel (up to four 32-row tiles), longer ones to a 256-row
+    tile; an expert of 257 rows is one whole tile plus a 1-row tail, 384 a
+    whole tile plus a 128-row tail, 385 two tiles. Every output row is
+    checked against the oracle."""
+    counts = [0, 1, 31, 32, 33, 64, 65, 100, 128, 129, 256, 257, 320, 384, 385, 528, 16]
     rng = np.random.default_rng(n + k + gated)
     E = len(counts)
     offs = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
