@@ -66,10 +66,13 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kXcds = 8;                 // MI355X: 8 XCDs, each with its own L2
 // Super-tiles per XCD: kSuper workgroups (one XCD's resident set) as
 // super_m row tiles x kSuper / super_m column tiles. Measured on config 8:
-// the gate and up GEMM ran 4% faster at 8 x 4 (or 16 x 2) than at 4 x 8 or
-// 2 x 16; the down GEMM varies by about 1% over all shapes, fastest at
-// 16 x 2. Shapes of more than 32 workgroups (16 x 4, 12 x 4) ran 10% slower.
-constexpr int kSuperMGated = 8;
+// with its experts' short tails in the thin kernel, each expert has 4 row
+// tiles, and the gate and up GEMM runs 2% faster per call at 4 x 8 (a
+// super-tile's rows are one expert's) than at 8 x 4; before, when the short
+// tails were further row tiles, 8 x 4 (or 16 x 2) had been 4% faster than
+// 4 x 8. The down GEMM varies by about 1% over all shapes, fastest at 16 x 2.
+// Shapes of more than 32 workgroups (16 x 4, 12 x 4) ran 10% slower.
+constexpr int kSuperMGated = 4;
 constexpr int kSuperMPlain = 16;
 constexpr int kSuper = 32;
 
@@ -127,9 +130,7 @@ __global__ __launch_bounds__(kThreads) void moe_expert_gemm_kernel(const GemmArg
     // takes super-tiles of super_m row tiles x kSuper / super_m column tiles
     // in turn, so its 32 resident workgroups share activation and weight
     // k-tiles in that XCD's L2. Row tiles enumerate (expert, tile) in expert
-    // order. Fewer workgroups per activation line (8 x 4 rather than 4 x 8)
-    // cut the gated GEMM's L2 hit rate from 72% to 62% but also its L1 -> L2
-    // latency from 508 to 438 cycles, and it ran 6% faster.
+    // order.
     const int xcd = blockIdx.x & (kXcds - 1);
     const int slot = blockIdx.x / kXcds;
     const int st = (slot / kSuper) * kXcds + xcd;     // super-tile
