@@ -372,7 +372,10 @@ int swiftllm_hip_moe_route_dispatch(const float* logits, const void* x,
  *   w2 != NULL: c[rows] = silu(a[rows] . w[e]^T) * (a[rows] . w2[e]^T)
  * w and w2 are fp16 [E, n, k]. fp32 accumulation. Supported (NotSupported
  * otherwise): n % 128 == 0 with w2, n % 256 == 0 without; k % 64 == 0 and
- * k <= 2^21; E <= 256. */
+ * k <= 2^21; E <= 256. expert_offsets runs non-decreasing from 0 to m_total
+ * (as the dispatch writes it): the grid is sized from m_total. Enqueues up
+ * to two kernels on `stream`: whole 256-row tiles, and the experts' tails
+ * of at most 128 rows (a decode batch: only the second). */
 int swiftllm_hip_moe_expert_gemm(const void* a, const void* w, const void* w2,
                                  const int32_t* expert_offsets,
                                  int num_experts, int m_total, int n, int k,
