@@ -74,6 +74,31 @@ def test_expert_gemm_thin_tails(dev, gated, n, k):
 
 
 @pytest.mark.parametrize("gated", [False, True])
+def test_expert_gemm_many_experts(dev, gated):
+    """160 experts: the main kernel's per-expert tile table is a wave scan in
+    chunks of 64 experts with a carry, so three chunks (the last partial)
+    meet here; counts from 0 to 600 rows give most experts a thin tail and
+    some whole tiles, at expert indices past 64 and 128."""
+    rng = np.random.default_rng(160 + gated)
+    E, n, k = 160, (128 if gated else 256), 128
+    counts = rng.integers(0, 40, E)
+    counts[rng.choice(E, 12, replace=False)] = rng.integers(200, 600, 12)
+    counts[[70, 150]] = [300, 513]   # whole tiles past the first and second chunk
+    offs = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    m_total = int(offs[-1])
+    a = (rng.standard_normal((m_total, k)) * 0.5).astype(np.float16)
+    w = (rng.standard_normal((E, n, k)) / np.sqrt(k)).astype(np.float16)
+    w2 = (rng.standard_normal((E, n, k)) / np.sqrt(k)).astype(np.float16) if gated else None
+    c = DeviceArray((m_total, n), np.float16)
+    c.fill_byte(0xFF)
+    moe.moe_expert_gemm(DeviceArray.from_numpy(a), DeviceArray.from_numpy(w),
+                        DeviceArray.from_numpy(w2) if gated else None, DeviceArray.from_numpy(offs), c)
+    synchronize()
+    _close(c.numpy().astype(np.float64), oracle.moe_expert_gemm(a, w, w2, offs),
+           f"160 experts gated={gated} rows={m_total}")
+
+
+@pytest.mark.parametrize("gated", [False, True])
 def test_expert_gemm_decode_batch(dev, gated):
     """A decode step's MoE: 64 tokens, top-2 of 8 experts, so every expert
     holds a few rows and the whole GEMM runs in the thin kernel (k 4096,
