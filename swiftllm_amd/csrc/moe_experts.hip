@@ -483,10 +483,24 @@ __device__ __forceinline__ void thin_tile(const GemmArgs& a, f16* lds, int e, in
 
     const int nk = a.k / kBK;
     constexpr int NS = C::NS;
-    // Stages 0 .. NS - 2 in flight; stages past the last reload the last one
+    // With a one-tile tail, workgroups start their k walk at different
+    // stages (and wrap), so that at any moment they read different k offsets
+    // of their rows: the weight rows of a stage sit k * 2 bytes apart (8 KiB
+    // for k = 4096), and the same offset in every row would load the same
+    // HBM channels. Step kt reads stage (kt + rot) % nk; the sum is the same
+    // set of stages. Longer tails keep an expert's workgroups in step, since
+    // they then share its many tail rows in L2. Measured (one box): 64-token
+    // decode batch 497 -> 489 us per call with the rotation; rotating every
+    // shape made a 512-token batch's down GEMM 208 -> 260 us.
+    const int rot = NTT == 1 ? static_cast<int>((blockIdx.x * 37u + blockIdx.y * 11u) %
+                                                static_cast<unsigned>(nk))
+                             : 0;
+    auto stage = [&](int kt) { const int s = kt + rot; return s >= nk ? s - nk : s; };
+    // Stages 0 .. NS - 2 in flight; steps past the last reload the last one
     // (in bounds, never read as a stage), so every step issues one stage.
 #pragma unroll
-    for (int s = 0; s < NS - 1; ++s) thin_issue<GATED, NTT>(lds, rx, rw, rw2, off, wv, min(s, nk - 1), s);
+    for (int s = 0; s < NS - 1; ++s)
+        thin_issue<GATED, NTT>(lds, rx, rw, rw2, off, wv, stage(min(s, nk - 1)), s);
     for (int kt = 0; kt < nk; ++kt) {
         wait_vm<(NS - 2) * C::L>();   // this wave's loads of stage kt landed
         // Everyone's, and everyone is done with stage kt - 1. The empty asm
@@ -496,8 +510,8 @@ __device__ __forceinline__ void thin_tile(const GemmArgs& a, f16* lds, int e, in
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
-        thin_issue<GATED, NTT>(lds, rx, rw, rw2, off, wv, min(kt + NS - 1, nk - 1),
-                               (kt + NS - 1) % NS);   // into stage kt - 1's buffer
+        thin_issue<GATED, NTT>(lds, rx, rw, rw2, off, wv, stage(min(kt + NS - 1, nk - 1)),
+                               (kt + NS - 1) % NS);   // into step kt - 1's buffer
         const f16* st = lds + static_cast<size_t>(kt % NS) * C::SH;
 #pragma unroll
         for (int ks = 0; ks < kBK / 16; ++ks) {
