@@ -93,7 +93,8 @@ def parse():
                     help="config 3: do not also time 512-token partitions in the same run (for "
                          "profiles whose per-kernel averages should cover the main workload only)")
     ap.add_argument("--kernel", default=None, help="kernel name substring for --summarize-pmc")
-    ap.add_argument("--alg-bytes", type=int, default=0, help="algorithmic bytes per call (--summarize-pmc)")
+    ap.add_argument("--alg-bytes", type=int, default=0,
+                    help="algorithmic bytes per launch of --kernel (--summarize-pmc)")
     ap.add_argument("--workload", default="", help="workload label (--summarize-pmc)")
     return ap.parse_args()
 
@@ -175,7 +176,7 @@ def summarize_pmc(fetch_dir, write_dir, kernel, alg_bytes, workload):
                        f"WRITE_SIZE {max(write[copy[0]]):.1f} KiB for {int(calib_kib)} KiB moved each way",
         "dispatches_averaged": len(fetch[name]),
         "other_kernels_same_call": others,
-        "algorithmic_bytes_per_call": alg_bytes or None,
+        "algorithmic_bytes_per_launch": alg_bytes or None,
     }
     print(json.dumps(rec, indent=1))
 
@@ -881,7 +882,9 @@ def bench_moe_decode(args):
                    "algorithmic_bytes_per_call": alg, "weight_bytes_per_call": weight_bytes,
                    "flops_per_call": 2 * rows * hidden * I * 3,
                    "kernels": "rank+route, permute, thin expert GEMM (gated), thin expert GEMM, combine"},
-        # traffic: HBM bytes per launch of the dominant kernel, the gated thin GEMM
+        # achieved: the whole call's algorithmic bytes / call time (all five kernels),
+        # a lower bound on the dominant kernel's own rate; traffic: HBM bytes per
+        # launch of the dominant kernel, the gated thin GEMM (1.88 GB of weights)
         "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(value / HBM_PEAK_GBS, 4),
                      "traffic": read_traffic("moe_decode_config10_traffic.json")},
@@ -933,6 +936,7 @@ def bench_moe_mlp(args):
         "config": {"workload": "mixtral-8x7b-moe-mlp", "num_tokens": T, "hidden": hidden,
                    "intermediate": I, "num_experts": E, "top_k": K, "flops_per_call": flops,
                    "kernels": "rank+route, permute, expert GEMM (gated), expert GEMM, combine"},
+        # achieved: the whole call's expert-GEMM flops / call time (all five kernels);
         # traffic: HBM bytes per launch of the dominant kernel, the gated GEMM
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
                      "frac": round(tflops / 2500.0, 4),

@@ -57,4 +57,4 @@ def test_summarize_pmc_scales_by_the_calibration_copy(tmp_path):
     assert rec["hbm_bytes_per_launch"] == (2000 * 2 + 20) * 1024
     assert rec["dispatches_averaged"] == 2
     assert rec["other_kernels_same_call"] == {"other(B)": {"fetch_kib": 7.0, "write_kib": 0.0}}
-    assert rec["algorithmic_bytes_per_call"] == 4096000
+    assert rec["algorithmic_bytes_per_launch"] == 4096000
