@@ -89,9 +89,13 @@ def parse():
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"), default=None,
                     help="no GPU work: print the HBM traffic JSON of --kernel from two rocprofv3 --pmc "
                          "runs (FETCH_SIZE, then WRITE_SIZE) of a bench command with --calib-copy-mib")
-    ap.add_argument("--skip-partition512", action="store_true",
-                    help="config 3: do not also time 512-token partitions in the same run (for "
+    ap.add_argument("--skip-side-partition", "--skip-partition512", dest="skip_partition512",
+                    action="store_true",
+                    help="config 3: do not also time 4096-token partitions beside BASELINE's 512 (for "
                          "profiles whose per-kernel averages should cover the main workload only)")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="config 2: leave out the sub-records of configs 1, 3, 4 and 5 that the default "
+                         "line carries (for profiles of config 2 alone)")
     ap.add_argument("--kernel", default=None, help="kernel name substring for --summarize-pmc")
     ap.add_argument("--alg-bytes", type=int, default=0,
                     help="algorithmic bytes per launch of --kernel (--summarize-pmc)")
@@ -206,7 +210,8 @@ def main():
     if args.ceiling:
         return bench_ceiling(args)
     if args.config == 5:
-        return bench_moe(args)
+        print(json.dumps(bench_moe(args)), flush=True)
+        return
     if args.config in (6, 7):
         return bench_blocks(args)
     if args.config == 8:
@@ -215,23 +220,48 @@ def main():
         return bench_prefill(args)
     if args.config == 10:
         return bench_moe_decode(args)
-    if args.rotate is None:
-        args.rotate = 4
-    if args.variant is None:
-        args.variant = "v1" if args.config in (1, 2) else "v2"
-    if args.partition is None:
-        # measured defaults: 4096-token partitions for both. Config 3 (long
-        # uniform contexts): 165 us, the same as 8192. Config 4 (ragged), with
-        # the split-K items started longest first: 175.7 us, against 177.4 at
-        # 2048, 182.0 at 1024 and 189.0 balanced
-        args.partition = 4096
+    rec = bench_decode(args, args.config, variant=args.variant, partition=args.partition)
+    if args.config == 2 and not args.no_configs:
+        rec["configs"] = other_configs(args, rec)
+    print(json.dumps(rec), flush=True)
+
+
+# Default partition sizes of the split-K configs. Config 3: BASELINE states
+# 512-token partitions (64 per sequence); the run also times 4096 beside it
+# (measured fastest for long uniform contexts: 165 us, the same as 8192).
+# Config 4 (ragged), with the split-K items started longest first: 4096 is
+# fastest (175.7 us, against 177.4 at 2048, 182.0 at 1024 and 189.0 balanced).
+DEFAULT_PARTITION = {3: 512, 4: 4096}
+SIDE_PARTITION = {3: 4096}
+
+
+def bench_decode(args, config, *, variant=None, partition=None, steps=None, warmup=None,
+                 samples=None, stream_gbs=None, log_prefix="[bench]"):
+    """One decode configuration (1-4) timed on its own inputs; returns its
+    JSON record. A step is one decode call (config 4: the cache write of the
+    step's new tokens, then the decode) with every input resident in HBM and
+    `--rotate` copies of the KV pool rotated between calls so no call finds
+    its K/V in the 256 MB Infinity Cache. `stream_gbs`, when given, is a
+    stream ceiling already measured in this process."""
+    from swiftllm_amd import _hip, workloads
+    from swiftllm_amd import paged_attention as pa
+    from swiftllm_amd._hip import DeviceArray, Event, Stream
+
+    steps = args.steps if steps is None else steps
+    warmup = args.warmup if warmup is None else warmup
+    samples = args.samples if samples is None else samples
+    rotate = 4 if args.rotate is None else args.rotate
+    if variant is None:
+        variant = "v1" if config in (1, 2) else "v2"
+    if partition is None:
+        partition = DEFAULT_PARTITION.get(config, 4096)
     t0 = time.time()
-    w = workloads.decode_config(args.config, seed=args.seed)
+    w = workloads.decode_config(config, seed=args.seed)
     sh = w.shape
     kv_bytes = w.kv_bytes()
     alg_bytes = kv_bytes + w.other_bytes()
-    print(f"[bench] workload generated in {time.time() - t0:.1f}s: S={sh['num_seqs']} "
-          f"sum(ctx)={int(w.context_lens.sum())} pool={sh['num_blocks']} blocks "
+    print(f"{log_prefix} config {config}: workload generated in {time.time() - t0:.1f}s: "
+          f"S={sh['num_seqs']} sum(ctx)={int(w.context_lens.sum())} pool={sh['num_blocks']} blocks "
           f"kv_bytes={kv_bytes / 1e6:.1f} MB", file=sys.stderr, flush=True)
 
     stream = Stream()
@@ -240,56 +270,59 @@ def main():
     ctx = DeviceArray.from_numpy(w.context_lens)
     out = DeviceArray(w.q.shape, np.float16)
     pools = [(DeviceArray.from_numpy(w.key_cache), DeviceArray.from_numpy(w.value_cache))
-             for _ in range(max(1, args.rotate))]
-    ws = None
-    if args.variant == "v2":
-        ws = pa.workspace(pa.paged_attention_v2_workspace_size(
-            sh["num_seqs"], sh["num_heads"], sh["num_kv_heads"], sh["head_dim"], sh["block_size"],
-            sh["max_num_blocks_per_seq"], args.partition), stream)
-
-    if args.config == 4:
+             for _ in range(max(1, rotate))]
+    slots = None
+    if config == 4:
         k_new = DeviceArray.from_numpy(w.new_key)
         v_new = DeviceArray.from_numpy(w.new_value)
         slots = DeviceArray.from_numpy(w.slot_mapping)
 
-    def step(i):
-        kc, vc = pools[i % len(pools)]
-        if args.config == 4:
-            pa.launch_reshape_and_cache(k_new, v_new, kc, vc, slots, sh["num_seqs"], sh["num_kv_heads"],
-                                        sh["head_dim"], sh["block_size"], num_blocks=sh["num_blocks"],
-                                        stream=stream)
-        if args.variant == "v2":
-            pa.paged_attention_v2(out, ws, q, kc, vc, bt, ctx, w.scale, sh["num_seqs"],
-                                  sh["num_heads"], sh["num_kv_heads"], sh["head_dim"],
-                                  sh["block_size"], sh["max_num_blocks_per_seq"], args.partition,
-                                  num_blocks=sh["num_blocks"], stream=stream)
-        else:
-            pa.paged_attention_v1(out, q, kc, vc, bt, ctx, w.scale, sh["num_seqs"],
-                                  sh["num_heads"], sh["num_kv_heads"], sh["head_dim"],
-                                  sh["block_size"], sh["max_num_blocks_per_seq"],
-                                  num_blocks=sh["num_blocks"], stream=stream)
+    def make_step(var, part):
+        ws = None
+        if var == "v2":
+            ws = pa.workspace(pa.paged_attention_v2_workspace_size(
+                sh["num_seqs"], sh["num_heads"], sh["num_kv_heads"], sh["head_dim"], sh["block_size"],
+                sh["max_num_blocks_per_seq"], part), stream)
 
-    for i in range(args.warmup):
+        def step(i):
+            kc, vc = pools[i % len(pools)]
+            if config == 4:
+                pa.launch_reshape_and_cache(k_new, v_new, kc, vc, slots, sh["num_seqs"],
+                                            sh["num_kv_heads"], sh["head_dim"], sh["block_size"],
+                                            num_blocks=sh["num_blocks"], stream=stream)
+            if var == "v2":
+                pa.paged_attention_v2(out, ws, q, kc, vc, bt, ctx, w.scale, sh["num_seqs"],
+                                      sh["num_heads"], sh["num_kv_heads"], sh["head_dim"],
+                                      sh["block_size"], sh["max_num_blocks_per_seq"], part,
+                                      num_blocks=sh["num_blocks"], stream=stream)
+            else:
+                pa.paged_attention_v1(out, q, kc, vc, bt, ctx, w.scale, sh["num_seqs"],
+                                      sh["num_heads"], sh["num_kv_heads"], sh["head_dim"],
+                                      sh["block_size"], sh["max_num_blocks_per_seq"],
+                                      num_blocks=sh["num_blocks"], stream=stream)
+        return step, ws
+
+    step, _ws = make_step(variant, partition)
+    for i in range(warmup):
         step(i)
     stream.synchronize()
-    print(f"[bench] warmup {args.warmup} done", file=sys.stderr, flush=True)
+    print(f"{log_prefix} config {config}: warmup {warmup} done", file=sys.stderr, flush=True)
 
     # Timed region: K back-to-back launches on one stream between two events.
     start, end = Event(), Event()
     _hip.synchronize()
     start.record(stream)
-    for i in range(args.steps):
+    for i in range(steps):
         step(i)
     end.record(stream)
     end.synchronize()
     _hip.synchronize()
-    total_ms = start.elapsed_ms(end)
-    ms = total_ms / args.steps
-    print(f"[bench] timed {args.steps} steps: {ms * 1e3:.2f} us/call", file=sys.stderr, flush=True)
+    ms = start.elapsed_ms(end) / steps
+    print(f"{log_prefix} config {config}: timed {steps} steps: {ms * 1e3:.2f} us/call",
+          file=sys.stderr, flush=True)
 
     # Per-launch distribution: each launch bracketed by its own events.
-    per = []
-    evs = [(Event(), Event()) for _ in range(args.samples)]
+    evs = [(Event(), Event()) for _ in range(samples)]
     for i, (a, b) in enumerate(evs):
         a.record(stream)
         step(i)
@@ -301,7 +334,7 @@ def main():
     # Single-launch latency: one call on an idle GPU (the stream drained before
     # and after), from its first event to its last.
     single = []
-    for i in range(args.samples and 20):
+    for i in range(samples and 20):
         a, b = Event(), Event()
         stream.synchronize()
         a.record(stream)
@@ -311,40 +344,36 @@ def main():
         single.append(a.elapsed_ms(b) * 1e3)
     single_p50 = float(np.median(single)) if single else None
 
-    # Config 3 as BASELINE states it (512-token partitions, 64 per sequence),
-    # timed beside the default in the same run.
-    ms512 = None
-    if args.config == 3 and args.variant == "v2" and args.partition != 512 and not args.skip_partition512:
-        ws512 = pa.workspace(pa.paged_attention_v2_workspace_size(
-            sh["num_seqs"], sh["num_heads"], sh["num_kv_heads"], sh["head_dim"], sh["block_size"],
-            sh["max_num_blocks_per_seq"], 512), stream)
-
-        def step512(i):
-            kc, vc = pools[i % len(pools)]
-            pa.paged_attention_v2(out, ws512, q, kc, vc, bt, ctx, w.scale, sh["num_seqs"],
-                                  sh["num_heads"], sh["num_kv_heads"], sh["head_dim"],
-                                  sh["block_size"], sh["max_num_blocks_per_seq"], 512,
-                                  num_blocks=sh["num_blocks"], stream=stream)
-
-        ms512 = timed(step512, stream, max(args.steps // 4, 1), min(args.warmup, 20), 0)[0]
+    # The other partition size of a split-K config, timed beside it in the
+    # same run on the same inputs.
+    side = None
+    side_part = SIDE_PARTITION.get(config)
+    if variant == "v2" and side_part is not None and side_part != partition and not args.skip_partition512:
+        side_step, _side_ws = make_step("v2", side_part)
+        ms_side = timed(side_step, stream, steps, min(warmup, 20), 0)[0]
+        side = {"partition_tokens": side_part, "us_per_call": round(ms_side * 1e3, 3),
+                "kv_gbs": round(kv_bytes / (ms_side * 1e-3) / 1e9, 2),
+                "hbm_peak_frac": round(alg_bytes / (ms_side * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        print(f"{log_prefix} config {config}: partition {side_part}: {ms_side * 1e3:.2f} us/call",
+              file=sys.stderr, flush=True)
 
     value = kv_bytes / (ms * 1e-3) / 1e9          # KV-read GB/s
     achieved = alg_bytes / (ms * 1e-3) / 1e9      # all algorithmic bytes / kernel time
-
-    traffic = read_traffic(f"decode_config{args.config}_traffic.json")
+    part_tag = f"_p{partition}" if (variant == "v2" and config == 3 and partition != 4096) else ""
+    traffic = read_traffic(f"decode_config{config}{part_tag}_traffic.json")
 
     # Ceilings measured in this run, after the timed calls (the store probe
     # overwrites cache contents): the same K/V tiles read by the gather
     # kernel alone (and for config 4 the cache write's stores alone), and the
     # NT sequential read stream.
-    ceiling = stream_gbs = None
-    if not args.no_ceiling:
-        ceiling = decode_ceiling(w, pools, bt, stream, max(args.steps // 4, 20), kv_bytes,
-                                 args.partition if args.variant == "v2" else 0,
-                                 slots if args.config == 4 else None)
-        stream_gbs = measure_stream(stream)[0]
-        print(f"[bench] ceiling {ceiling['value']:.0f} GB/s ({ceiling['us_per_call']:.2f} us), "
-              f"stream {stream_gbs:.0f} GB/s", file=sys.stderr, flush=True)
+    ceiling = None
+    if not args.no_ceiling and config != 1:
+        ceiling = decode_ceiling(w, pools, bt, stream, max(steps // 4, 20), kv_bytes,
+                                 partition if variant == "v2" else 0, slots)
+        if stream_gbs is None:
+            stream_gbs = measure_stream(stream)[0]
+        print(f"{log_prefix} config {config}: ceiling {ceiling['value']:.0f} GB/s "
+              f"({ceiling['us_per_call']:.2f} us), stream {stream_gbs:.0f} GB/s", file=sys.stderr, flush=True)
 
     cpu = None
     if not args.no_cpu:
@@ -361,22 +390,22 @@ def main():
         cpu_s = float(np.median(times))
         cpu = {"value": round(kv_bytes / cpu_s / 1e9, 3), "unit": "GB/s", "cores": int(threads),
                "kind": "port", "us_per_call": round(cpu_s * 1e6, 1), **host_info(),
-               "sample": f"full config-{args.config} batch (same inputs, decode only), fp32 C restatement "
+               "sample": f"full config-{config} batch (same inputs, decode only), fp32 C restatement "
                          f"(oracle/oracle.c, OpenMP over (seq, kv head)), median of {len(times)} runs"}
-        print(f"[bench] cpu baseline {cpu_s * 1e3:.1f} ms/call on {threads} threads", file=sys.stderr,
-              flush=True)
+        print(f"{log_prefix} config {config}: cpu baseline {cpu_s * 1e3:.1f} ms/call on {threads} threads",
+              file=sys.stderr, flush=True)
 
     workload_name = {1: "tiny-mha-decode", 2: "llama3-8b-decode-layer", 3: "llama3-70b-long-context-splitk",
-                     4: "ragged-continuous-batching-step"}[args.config]
+                     4: "ragged-continuous-batching-step"}[config]
     ctx_desc = {1: "uniform[1,256]", 2: "uniform[512,4096]", 3: "32768 (all)",
-                4: "lognormal(median 600, sigma 1) clip [1,8192]"}[args.config]
+                4: "lognormal(median 600, sigma 1) clip [1,8192]"}[config]
     rec = {
         "metric": "paged-attn decode KV-read GB/s (% HBM peak) + us/call @ Llama-3-8B shape",
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": round(ms, 6),
         "us_per_call": round(ms * 1e3, 3),
         "us_per_call_p10_p50_p90": [round(p10, 2), round(p50, 2), round(p90, 2)],
@@ -393,8 +422,8 @@ def main():
             "num_kv_heads": sh["num_kv_heads"], "head_dim": sh["head_dim"],
             "block_size": sh["block_size"], "context_lens": ctx_desc,
             "sum_context": int(w.context_lens.sum()), "pool_blocks": sh["num_blocks"],
-            "kernel": f"paged_attention_{args.variant}" + (f"/partition{args.partition}" if args.variant == "v2" else "")
-                      + ("+reshape_and_cache" if args.config == 4 else ""),
+            "kernel": f"paged_attention_{variant}" + (f"/partition{partition}" if variant == "v2" else "")
+                      + ("+reshape_and_cache" if config == 4 else ""),
             "kv_pool_copies_rotated": len(pools), "seed": args.seed,
             "kv_bytes_per_call": kv_bytes, "algorithmic_bytes_per_call": alg_bytes,
         },
@@ -412,7 +441,9 @@ def main():
         "stream_frac": round(value / stream_gbs, 4) if stream_gbs else None,
         "cpu_baseline": cpu,
     }
-    if args.config == 1:
+    if variant == "v2":
+        rec["config"]["partition_tokens"] = partition
+    if config == 1:
         # latency-bound (1 MB per call): us/call only, no roofline claim
         rec["metric"] = "paged-attn decode us/call @ tiny MHA (BASELINE config 1, CPU-runnable case)"
         rec["value"], rec["unit"], rec["higher_is_better"] = round(ms * 1e3, 3), "us", False
@@ -420,10 +451,32 @@ def main():
         rec["ceiling_frac"] = rec["stream_frac"] = None
         if cpu:
             cpu.update(value=cpu["us_per_call"], unit="us")
-    if ms512 is not None:
-        rec["us_per_call_partition512"] = round(ms512 * 1e3, 3)
-        rec["kv_gbs_partition512"] = round(kv_bytes / (ms512 * 1e-3) / 1e9, 2)
-    print(json.dumps(rec), flush=True)
+    if side is not None:
+        rec[f"partition{side['partition_tokens']}"] = side
+    return rec
+
+
+# Keys of a configuration's record that the line's own header already states.
+_SUB_DROP = ("n_gpus", "scaling", "vs_baseline", "higher_is_better", "steps", "warmup")
+
+
+def other_configs(args, main_rec):
+    """BASELINE configs 1, 3, 4 and 5, each on its own seeded inputs, timed in
+    this process after the headline config 2, as sub-records of its line:
+    us/call, the roofline of the algorithmic bytes against 8 TB/s with the
+    committed HBM traffic, the live ceiling of the call's own access pattern,
+    and the CPU restatement on this host. Config 3 runs at BASELINE's
+    512-token partitions, with 4096-token partitions timed beside it."""
+    stream_gbs = main_rec.get("stream_read_gbs")
+    subs = {}
+    for cfg in (1, 3, 4, 5):
+        if cfg == 5:
+            rec = bench_moe(args, stream_gbs=stream_gbs, log_prefix="[bench]")
+        else:
+            rec = bench_decode(args, cfg, stream_gbs=stream_gbs)
+        rec["steps_timed"] = rec.get("steps")
+        subs[str(cfg)] = {k: v for k, v in rec.items() if k not in _SUB_DROP}
+    return subs
 
 
 def calibrate(nbytes):
@@ -692,10 +745,12 @@ def bench_ceiling(args):
     print(json.dumps(rec), flush=True)
 
 
-def bench_moe(args):
+def bench_moe(args, stream_gbs=None, log_prefix="[bench]"):
     """Config 5: Mixtral-8x7B-style routing + dispatch (4096 tokens, hidden 4096,
     8 experts, top-2). Eight copies of the activations and outputs rotate so
-    the 256 MB Infinity Cache cannot hold a call's 100.9 MB."""
+    the 256 MB Infinity Cache cannot hold a call's 100.9 MB. Returns the JSON
+    record; `stream_gbs`, when given, is a stream ceiling already measured in
+    this process."""
     from swiftllm_amd import moe, workloads
     from swiftllm_amd._hip import DeviceArray, Stream
 
@@ -723,11 +778,13 @@ def bench_moe(args):
     ms, p10, p50, p90 = timed(step, stream, args.steps, args.warmup, args.samples)
     alg = wl.bytes()
     value = alg / (ms * 1e-3) / 1e9
+    print(f"{log_prefix} config 5: timed {args.steps} steps: {ms * 1e3:.2f} us/call "
+          f"(route then dispatch: {ms2 * 1e3:.2f})", file=sys.stderr, flush=True)
 
     # Ceiling measured in this run: the call's row copies alone (each row read
     # once, written to its top-k destinations at the rows the dispatch chose),
     # over the same rotated buffers; and the NT sequential read stream.
-    ceiling = stream_gbs = None
+    ceiling = None
     if not args.no_ceiling:
         from swiftllm_amd import ceilings
 
@@ -742,7 +799,8 @@ def bench_moe(args):
                               "NT loads and stores, destinations from the dispatch)",
                    "value": round(alg / (t_copy * 1e-6) / 1e9, 2), "unit": "GB/s",
                    "us_per_call": round(t_copy, 3)}
-        stream_gbs = measure_stream(stream)[0]
+        if stream_gbs is None:
+            stream_gbs = measure_stream(stream)[0]
     cpu = None
     if not args.no_cpu:
         import oracle
@@ -781,7 +839,7 @@ def bench_moe(args):
         "stream_frac": round(value / stream_gbs, 4) if stream_gbs else None,
         "cpu_baseline": cpu,
     }
-    print(json.dumps(rec), flush=True)
+    return rec
 
 
 def bench_prefill(args):
