@@ -549,7 +549,7 @@ def measure_gather(w, pools, bt, stream, steps, load_bytes, partition_tokens):
 
     def step(i):
         kc, vc = pools[i % len(pools)]
-        ceilings.tile_gather(kc, vc, bt, d_items, len(items), Hkv, sh["head_dim"],
+        ceilings.tile_gather(kc, vc, bt, d_items, len(items), sh["num_seqs"], Hkv, sh["head_dim"],
                              sh["max_num_blocks_per_seq"], sh["num_blocks"], load_bytes, sink, stream)
 
     return timed(step, stream, steps, 10, 0)[0] * 1e3

@@ -58,11 +58,13 @@ int swiftllm_ceil_read_stream(const void* src, size_t bytes, uint32_t* sink,
  * kv head h at block_tables[s, first .. end - 1] (end clipped to
  * max_num_blocks_per_seq). One 4-wave workgroup per item, in item order,
  * waves taking blocks round-robin, two blocks per wave in flight.
- * load_bytes 8 or 16; head_dim 64 or 128; block ids outside [0, num_blocks)
- * are skipped (num_blocks <= 0: no bound). */
+ * load_bytes 8 or 16; head_dim 64 or 128. Items whose unit is negative or
+ * names a sequence s >= num_seqs (rows of block_tables) read nothing;
+ * block ids outside [0, num_blocks) are skipped (num_blocks <= 0: no
+ * bound). */
 int swiftllm_ceil_tile_gather(const void* key_cache, const void* value_cache,
                               const int32_t* block_tables, const int32_t* items,
-                              int num_items, int num_kv_heads, int head_dim,
+                              int num_items, int num_seqs, int num_kv_heads, int head_dim,
                               int max_num_blocks_per_seq, int num_blocks,
                               int load_bytes, uint32_t* sink,
                               hipStream_t stream);

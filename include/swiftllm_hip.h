@@ -163,15 +163,21 @@ int swiftllm_hip_launch_reshape_and_cache(
     int block_size, int num_blocks, hipStream_t stream);
 
 /* Bytes of the static device scratch behind
- * swiftllm_hip_launch_paged_attention_v2_noalloc (one copy per device). */
+ * swiftllm_hip_launch_paged_attention_v2_noalloc (one copy per device). The
+ * array is part of libswiftllm_hip.so's code object, so every process that
+ * runs any kernel of the library on a device holds these 64 MiB there from
+ * the code object's load until the process ends, whether or not it ever
+ * calls the no-alloc entry point. */
 #define SWIFTLLM_HIP_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 
 /* No counterpart in the reference. For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): swiftllm_hip_launch_paged_attention_v2 without the
  * workspace arguments. Its split-K scratch is a static device array of
- * SWIFTLLM_HIP_NOALLOC_SCRATCH_BYTES bytes that each device holds from its
- * first call until the process ends; nothing is allocated or freed per call.
+ * SWIFTLLM_HIP_NOALLOC_SCRATCH_BYTES bytes, reserved on each device when
+ * the library's code object loads there (first use of any of its kernels)
+ * and held until the process ends; the first call on a device looks up the
+ * array's address, and nothing is allocated or freed per call.
  * Sizes whose workspace (swiftllm_hip_paged_attention_v2_workspace_size for
  * the mode the call runs) exceeds that return SWIFTLLM_ERR_INVALID_PARAMETER.
  * All calls on one device share the array: calls that overlap on a device

@@ -22,7 +22,7 @@ sz = ctypes.c_size_t
 
 SIGNATURES = {
     "swiftllm_ceil_read_stream": (i32, [vp, sz, vp, vp]),
-    "swiftllm_ceil_tile_gather": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]),
+    "swiftllm_ceil_tile_gather": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp, vp]),
     "swiftllm_ceil_cache_store": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, vp]),
     "swiftllm_ceil_row_copy": (i32, [vp, vp, vp, i32, i32, i32, i32, vp]),
     "swiftllm_ceil_mfma_stream": (i32, [vp, sz, i32, i32, vp, vp]),
@@ -63,10 +63,10 @@ def read_stream(src, nbytes: int, sink, stream=None) -> None:
     _check(lib().swiftllm_ceil_read_stream(src.ptr, nbytes, sink.ptr, _h(stream)), "read_stream")
 
 
-def tile_gather(kc, vc, bt, items, num_items: int, num_kv_heads: int, head_dim: int,
+def tile_gather(kc, vc, bt, items, num_items: int, num_seqs: int, num_kv_heads: int, head_dim: int,
                 max_num_blocks_per_seq: int, num_blocks: int, load_bytes: int, sink,
                 stream=None) -> None:
-    _check(lib().swiftllm_ceil_tile_gather(kc.ptr, vc.ptr, bt.ptr, items.ptr, num_items,
+    _check(lib().swiftllm_ceil_tile_gather(kc.ptr, vc.ptr, bt.ptr, items.ptr, num_items, num_seqs,
                                            num_kv_heads, head_dim, max_num_blocks_per_seq,
                                            num_blocks, load_bytes, sink.ptr, _h(stream)),
            "tile_gather")

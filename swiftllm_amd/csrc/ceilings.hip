@@ -108,6 +108,7 @@ struct GatherArgs {
     const int* bt;
     const int* items;  // [n][3]
     uint32_t* sink;
+    int S;
     int Hkv;
     int MB;
     int num_blocks;
@@ -122,6 +123,7 @@ __global__ __launch_bounds__(256) void tile_gather_kernel(const GatherArgs a) {
     const int unit = item[0];
     const int s = unit / a.Hkv;
     const int h = unit - s * a.Hkv;
+    if (unit < 0 || s >= a.S) return;  // no row of the block table
     const int first = max(item[1], 0);
     const int end = min(item[2], a.MB);
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
@@ -328,9 +330,11 @@ int swiftllm_ceil_read_stream(const void* src, size_t bytes, uint32_t* sink, hip
 
 int swiftllm_ceil_tile_gather(const void* key_cache, const void* value_cache,
                               const int32_t* block_tables, const int32_t* items, int num_items,
-                              int num_kv_heads, int head_dim, int max_num_blocks_per_seq,
+                              int num_seqs, int num_kv_heads, int head_dim, int max_num_blocks_per_seq,
                               int num_blocks, int load_bytes, uint32_t* sink, hipStream_t stream) {
-    if (num_items < 0 || num_kv_heads <= 0 || max_num_blocks_per_seq < 0) return kErrInvalid;
+    if (num_items < 0 || num_seqs < 0 || num_kv_heads <= 0 || max_num_blocks_per_seq < 0) {
+        return kErrInvalid;
+    }
     if ((head_dim != 64 && head_dim != 128) || (load_bytes != 8 && load_bytes != 16)) {
         return kErrUnsupported;
     }
@@ -340,7 +344,7 @@ int swiftllm_ceil_tile_gather(const void* key_cache, const void* value_cache,
         return kErrInvalid;
     }
     GatherArgs a{static_cast<const char*>(key_cache), static_cast<const char*>(value_cache),
-                 block_tables, items, sink, num_kv_heads, max_num_blocks_per_seq, num_blocks};
+                 block_tables, items, sink, num_seqs, num_kv_heads, max_num_blocks_per_seq, num_blocks};
     auto k = head_dim == 128 ? (load_bytes == 16 ? tile_gather_kernel<128, 16> : tile_gather_kernel<128, 8>)
                              : (load_bytes == 16 ? tile_gather_kernel<64, 16> : tile_gather_kernel<64, 8>);
     return launch(k, dim3(num_items), dim3(256), stream, a);

@@ -144,6 +144,19 @@ __device__ __forceinline__ int sequence_for_block(const int* ctx, int S, int r) 
     return s_seq;
 }
 
+// Dynamic LDS of decode_item's wave merge, in floats: per wave 16 maxima,
+// 16 sums and gstride = min(G, 16) rows of D partial outputs.
+template <int D, int NW>
+__host__ __device__ constexpr int merge_lds_floats(int G) {
+    return NW * 32 + NW * (G < 16 ? G : 16) * D;
+}
+
+// Bytes of the partition kernel's item list for S sequences (int prefix of
+// S + 1 entries, 16-bit sequence list of S), rounded to 16.
+__host__ __device__ constexpr size_t part_list_lds_bytes(int S) {
+    return ((static_cast<size_t>(S) + 1) * 4 + static_cast<size_t>(S) * 2 + 15) / 16 * 16;
+}
+
 // One (sequence, kv head, head chunk, partition) item. The NW waves of the
 // workgroup take the item's blocks round-robin and merge through LDS; the
 // result is the output (single pass, or a sequence with one partition) or a
@@ -336,8 +349,13 @@ void paged_partition_kernel(const DecodeArgs a) {
         return;
     }
     constexpr int kPacked = kLptClasses / 2;
-    __shared__ int s_pre[kPartMaxSeqs + 1];          // exclusive prefix of full partitions
-    __shared__ unsigned short s_part[kPartMaxSeqs];  // sequences with a partial, longest first
+    // The item list sits in dynamic LDS after decode_item's merge area,
+    // sized by the host for this batch (part_list_lds_bytes): s_pre[S + 1]
+    // exclusive prefix of full partitions, s_part[S] sequences with a
+    // partial partition, longest first.
+    extern __shared__ __align__(16) float smem[];
+    int* s_pre = reinterpret_cast<int*>(smem + merge_lds_floats<D, NW>(a.G));
+    unsigned short* s_part = reinterpret_cast<unsigned short*>(s_pre + a.S + 1);
     __shared__ int s_wpk[NW][kPacked];               // per-wave class counts of a chunk
     __shared__ int s_cls[kLptClasses];               // next list position of each class
     __shared__ int s_wave[NW];
@@ -1024,9 +1042,7 @@ constexpr int kWavesV2 = SWIFTLLM_WAVES_V2;
 
 template <int D, int NW>
 hipError_t launch_decode_t(const DecodeArgs& a, int S, int mp_grid, hipStream_t stream) {
-    const int gstride = a.G < 16 ? a.G : 16;
-    const size_t lds = static_cast<size_t>(NW) * 32 * sizeof(float) +
-                       static_cast<size_t>(NW) * gstride * D * sizeof(float);
+    const size_t lds = static_cast<size_t>(merge_lds_floats<D, NW>(a.G)) * sizeof(float);
     dim3 grid(mp_grid, a.Hkv * a.nhc, S);
     return launch(paged_decode_kernel<D, NW>, grid, dim3(NW * 64), lds, stream, a);
 }
@@ -1039,9 +1055,8 @@ hipError_t launch_decode(const DecodeArgs& a, int D, int S, int mp_grid, hipStre
 
 template <int D, int NW>
 hipError_t launch_partition_t(const DecodeArgs& a, unsigned grid, hipStream_t stream) {
-    const int gstride = a.G < 16 ? a.G : 16;
-    const size_t lds = static_cast<size_t>(NW) * 32 * sizeof(float) +
-                       static_cast<size_t>(NW) * gstride * D * sizeof(float);
+    size_t lds = static_cast<size_t>(merge_lds_floats<D, NW>(a.G)) * sizeof(float);
+    if (a.S <= kPartMaxSeqs) lds += part_list_lds_bytes(a.S);
     return launch(paged_partition_kernel<D, NW>, dim3(grid), dim3(NW * 64), lds, stream, a);
 }
 

@@ -37,10 +37,12 @@ def test_validation_before_launch():
     L = ceilings.lib()
     assert L.swiftllm_ceil_read_stream(FAKE + 8, 4096, FAKE, None) == -4          # misaligned
     assert L.swiftllm_ceil_read_stream(FAKE, 4095, FAKE, None) == -4              # not 16-byte sized
-    assert L.swiftllm_ceil_tile_gather(FAKE, FAKE, FAKE, FAKE, 4, 8, 96, 16, 0, 16, FAKE,
+    assert L.swiftllm_ceil_tile_gather(FAKE, FAKE, FAKE, FAKE, 4, 2, 8, 96, 16, 0, 16, FAKE,
                                        None) == -6                                # head_dim 96
-    assert L.swiftllm_ceil_tile_gather(FAKE, FAKE, FAKE, FAKE, 4, 8, 128, 16, 0, 4, FAKE,
+    assert L.swiftllm_ceil_tile_gather(FAKE, FAKE, FAKE, FAKE, 4, 2, 8, 128, 16, 0, 4, FAKE,
                                        None) == -6                                # 4-byte loads
+    assert L.swiftllm_ceil_tile_gather(FAKE, FAKE, FAKE, FAKE, 4, -1, 8, 128, 16, 0, 16, FAKE,
+                                       None) == -4                                # negative num_seqs
     assert L.swiftllm_ceil_cache_store(FAKE, FAKE, FAKE, 4, 8, 128, 0, 3, None) == -4  # mode 3
     assert L.swiftllm_ceil_row_copy(FAKE, FAKE, FAKE, 4, 2, 4000, 8, None) == -6  # hidden % 512
     assert L.swiftllm_ceil_mfma_stream(FAKE, 512, 4, 4, FAKE, None) == -4         # < one fragment

@@ -7,6 +7,10 @@ same inputs (the same kernels run; only the scratch address differs), and
 stay within the attention tolerance of the fp64 oracle. Calls follow each
 other on one stream, the later ones smaller, so each runs over the scratch
 contents the previous one left. Sizes beyond the static scratch are refused.
+The first test makes the process's first no-alloc call inside stream capture
+(the device address of the static scratch is looked up on that call), so it
+must stay first in this file, and this file must run after every other test
+that could call the entry.
 """
 
 import ctypes
@@ -19,7 +23,7 @@ from helpers import assert_attention_close
 from swiftllm_amd import _lib
 from swiftllm_amd import paged_attention as pa
 from swiftllm_amd import workloads
-from swiftllm_amd._hip import DeviceArray, Stream
+from swiftllm_amd._hip import DeviceArray, Graph, Stream
 
 pytestmark = pytest.mark.gpu
 
@@ -65,6 +69,37 @@ class _Case:
         w = self.w
         return oracle.decode_f64(w.q, w.key_cache, w.value_cache, w.block_tables, w.context_lens,
                                  w.scale)
+
+
+def test_noalloc_first_call_captured_in_a_graph(dev):
+    """The first no-alloc call of the process is captured into a HIP graph.
+    Three replays, each after an eager no-alloc call on other inputs that
+    overwrites the shared scratch, must equal the workspace entry point's
+    output bit for bit."""
+    stream = Stream()
+    case = _Case(workloads.decode_config(3, seed=33, ctx=4096, num_seqs=4))
+    other = _Case(workloads.decode_config(1, seed=34, num_seqs=5))
+    out = DeviceArray(case.w.q.shape, np.float16)
+    status = []
+
+    def enqueue():
+        status.append(_lib.lib().swiftllm_hip_launch_paged_attention_v2_noalloc(
+            out.ptr, *case.args(), 512, case.sh["num_blocks"], stream.handle))
+
+    graph = Graph(stream, enqueue)
+    assert status == [0], _lib.last_error()
+    want, ws = case.with_workspace(512, stream)
+    stream.synchronize()
+    r = want.numpy()
+    for rep in range(3):
+        other.noalloc(64, stream)
+        out.fill_byte(0xFF)
+        graph.launch(stream)
+        stream.synchronize()
+        g = out.numpy()
+        assert np.array_equal(g.view(np.uint16), r.view(np.uint16)), f"replay {rep} differs"
+    assert_attention_close(g, case.ref(), "noalloc captured, config 3 heads, 4 x 4096 tokens")
+    ws.free()
 
 
 def test_noalloc_matches_workspace_entry_on_consecutive_calls(dev):
