@@ -67,6 +67,10 @@ struct DecodeArgs {
     int MP;           // partitions per sequence in the workspace
     int S;            // sequences
     int snake;        // > 0: single-pass item order in snake rounds of this many
+    // Partition streams (paged_partition_stream_kernel) only:
+    float* frag;      // [W][kFragHead + gstride * D]: the piece a wave's range starts with
+    int* meta;        // [0] blocks per team q, [1] teams, [2 .. S + 2] block prefix
+    int W;            // waves in the grid
 };
 
 // Attends `count` blocks of one sequence: logical blocks first,
@@ -718,8 +722,9 @@ struct StreamArgs {
 
 // Blocks per sequence -> exclusive prefix in s_pre[0..S] (s_pre[S] = total),
 // clamped context lengths in s_len. All threads of the workgroup take part.
-__device__ __forceinline__ void stream_prefix(const StreamArgs& a, int* s_pre, int* s_len,
-                                              int* s_tot) {
+// A: any argument struct with S, ctx and MB.
+template <typename A>
+__device__ __forceinline__ void stream_prefix(const A& a, int* s_pre, int* s_len, int* s_tot) {
     const int chunk = (a.S + blockDim.x - 1) / blockDim.x;
     const int c0 = threadIdx.x * chunk;
     int run = 0;
@@ -935,6 +940,342 @@ __global__ __launch_bounds__(256) void paged_streamk_reduce_kernel(const StreamR
         [&](int d, float v) { o[d] = static_cast<f16>(v); });
 }
 
+// ---------------------------------------------------------------------------
+// Split-K in partition streams. The blocks of all sequences form one list,
+// sequence by sequence, as in the balanced mode; a team of TS = Hkv * nhc
+// consecutive waves takes blocks [t*q, (t+1)*q) of it, each wave one kv head
+// and head chunk, so every wave gets the same number of blocks whatever the
+// context lengths. A wave walks its range with one continuous load pipeline
+// (the next block's tiles are in flight while a block is attended) and
+// leaves a partial (max, sum, normalised output) each time it reaches the
+// end of a partition: no LDS merge, no barrier and no pipeline drain per
+// partition, which is what the per-item walk pays over short partitions.
+// A range boundary t*q that falls strictly inside a partition splits it into
+// pieces. Only a wave's first piece can start at such a boundary; every
+// other piece starts at a partition start. A piece from a partition's start
+// goes to the partition's slot of the regular workspace, a piece from a
+// boundary to the boundary slot of wave (t, member) in `frag`. A sequence
+// with one partition and no boundary inside writes its output directly.
+// paged_reduce_pstream_* combine, per head, the partition slots and the
+// boundary slots that fall inside the sequence.
+// ---------------------------------------------------------------------------
+
+// A wave-uniform pointer held in SGPRs at this point of the program: the
+// empty asm hides its value from the optimiser, so address arithmetic on it
+// is done where it is used instead of being hoisted into a loop-invariant
+// 64-bit vector register pair.
+__device__ __forceinline__ char* pinned_sgpr(char* p) {
+    asm volatile("" : "+s"(p));
+    return p;
+}
+
+// Attends blocks j0 .. j1 - 1 of one sequence in order, double-buffered like
+// attend_blocks, and calls done(j) after block j; the next block's loads are
+// in flight while done(j) runs.
+template <int D, typename Done>
+__device__ __forceinline__ void attend_run(WaveState<D>& st, const const_int* btrow, int j0, int j1,
+                                           int L, const f16* kc, const f16* vc, int Hkv,
+                                           int num_blocks, int kvh, int loff, int kg,
+                                           const QOperand<D>& qB, h4 ident, float scale_log2,
+                                           Done done) {
+    constexpr int NJ = D / 16;
+    const int count = j1 - j0;
+    if (count <= 0) return;
+    auto block_at = [&](int j) { return __builtin_amdgcn_readfirstlane(btrow[j]); };
+    auto valid_of = [&](int j, int b) {
+        return block_ok(b, num_blocks) ? min(kBlockTokens, L - j * kBlockTokens) : 0;
+    };
+    h4 kA[NJ], vA[NJ], kB[NJ], vB[NJ];
+    int jA = j0;
+    int bA = block_at(jA);
+    load_tile<D>(kc, vc, Hkv, num_blocks, bA, kvh, loff, kA, vA);
+    int left = count;
+    for (; left > 2; left -= 2) {
+        const int jB = jA + 1;
+        const int bB = block_at(jB);
+        load_tile<D>(kc, vc, Hkv, num_blocks, bB, kvh, loff, kB, vB);
+        attend_block<D>(st, valid_of(jA, bA), kg, kA, vA, qB, ident, scale_log2);
+        done(jA);
+        jA = jB + 1;
+        bA = block_at(jA);
+        load_tile<D>(kc, vc, Hkv, num_blocks, bA, kvh, loff, kA, vA);
+        attend_block<D>(st, valid_of(jB, bB), kg, kB, vB, qB, ident, scale_log2);
+        done(jB);
+    }
+    if (left == 2) {
+        const int jB = jA + 1;
+        const int bB = block_at(jB);
+        load_tile<D>(kc, vc, Hkv, num_blocks, bB, kvh, loff, kB, vB);
+        attend_block<D>(st, valid_of(jA, bA), kg, kA, vA, qB, ident, scale_log2);
+        done(jA);
+        attend_block<D>(st, valid_of(jB, bB), kg, kB, vB, qB, ident, scale_log2);
+        done(jB);
+    } else {
+        attend_block<D>(st, valid_of(jA, bA), kg, kA, vA, qB, ident, scale_log2);
+        done(jA);
+    }
+}
+
+// Partition streams serve partitions of up to kPStreamMaxPartBlocks blocks,
+// in batches whose block prefix fits in LDS, with a grid of
+// kPStreamWavesPerSimd waves per SIMD (the kernel's register cap).
+#ifndef SWIFTLLM_PSTREAM_MAX_PART_BLOCKS
+#define SWIFTLLM_PSTREAM_MAX_PART_BLOCKS 64
+#endif
+#ifndef SWIFTLLM_PSTREAM_WAVES_PER_SIMD
+#define SWIFTLLM_PSTREAM_WAVES_PER_SIMD 2
+#endif
+constexpr int kPStreamMaxPartBlocks = SWIFTLLM_PSTREAM_MAX_PART_BLOCKS;
+constexpr int kPStreamWavesPerSimd = SWIFTLLM_PSTREAM_WAVES_PER_SIMD;
+
+// Teams of a partition-stream grid of W waves, TS waves per team.
+__host__ __device__ __forceinline__ int pstream_teams(int W, int TS) { return max(1, W / TS); }
+
+template <int D>
+__global__ __launch_bounds__(64 * kStreamWaves) __attribute__((amdgpu_waves_per_eu(kPStreamWavesPerSimd)))
+void paged_partition_stream_kernel(const DecodeArgs a) {
+    constexpr int NJ = D / 16;
+    extern __shared__ int s_dyn[];
+    int* s_pre = s_dyn;              // [S + 1]
+    int* s_len = s_dyn + a.S + 1;    // [S]
+    __shared__ int s_tot[64 * kStreamWaves];
+    stream_prefix(a, s_pre, s_len, s_tot);
+
+    const int U = __builtin_amdgcn_readfirstlane(s_pre[a.S]);
+    const int P = a.part_blocks;
+    const int TS = a.Hkv * a.nhc;
+    const int teams = pstream_teams(a.W, TS);
+    const int q = (U + teams - 1) / teams;
+    if (blockIdx.x == 0) {
+        // For the reduce: blocks per team, teams, and the block prefix.
+        for (int i = threadIdx.x; i <= a.S; i += blockDim.x) a.meta[2 + i] = s_pre[i];
+        if (threadIdx.x == 0) {
+            a.meta[0] = q;
+            a.meta[1] = teams;
+        }
+    }
+    // Sequences without blocks are not in the list: zero their outputs here.
+    for (int sz = blockIdx.x; sz < a.S; sz += gridDim.x) {
+        if (s_pre[sz + 1] == s_pre[sz]) {
+            for (int i = threadIdx.x; i < a.H * D; i += blockDim.x) {
+                a.out[static_cast<size_t>(sz) * a.H * D + i] = static_cast<f16>(0.0f);
+            }
+        }
+    }
+
+    const int lane = threadIdx.x & 63;
+    const int w = blockIdx.x * kStreamWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int team = w / TS;
+    if (team >= teams || U == 0) return;
+    const int member = w - team * TS;
+    const int r = lane & 15;
+    const int kg = lane >> 4;
+    const int gstride = min(16, a.G);
+    const int kvh = member / a.nhc;
+    const int hc = member - kvh * a.nhc;
+    const int g0 = hc * 16;
+    const int gn = min(16, a.G - g0);
+    const int h0 = kvh * a.G + g0;
+    const int u0 = min(U, team * q);
+    const int u1 = min(U, u0 + q);
+
+    h4 ident;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        ident[i] = (4 * kg + i == r) ? static_cast<f16>(1.0f) : static_cast<f16>(0.0f);
+    }
+    const int loff = kv_elem_offset(r, 4 * kg);
+
+    int u = u0;
+    while (u < u1) {
+        // Sequence of block u: the largest s with s_pre[s] <= u. Wave-uniform
+        // values go through readfirstlane so the block-table reads stay
+        // scalar loads.
+        int lo = 0, hi = a.S;
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (s_pre[mid] <= u) lo = mid; else hi = mid;
+        }
+        const int s = __builtin_amdgcn_readfirstlane(lo);
+        const int L = __builtin_amdgcn_readfirstlane(s_len[s]);
+        const int pre = __builtin_amdgcn_readfirstlane(s_pre[s]);
+        const int nb = __builtin_amdgcn_readfirstlane(s_pre[s + 1]) - pre;
+        const int j0 = u - pre;
+        const int j1 = min(nb, u1 - pre);
+        const int nparts = (nb + P - 1) / P;
+
+        QOperand<D> qB;
+        {
+            const f16* qp = a.q + (static_cast<size_t>(s) * a.H + h0 + min(r, gn - 1)) * D + 4 * kg;
+#pragma unroll
+            for (int J = 0; J < NJ; ++J) {
+                const h4 v = *reinterpret_cast<const h4*>(qp + 16 * J);
+                qB.v[J] = (r < gn) ? v : h4{0, 0, 0, 0};
+            }
+        }
+        const const_int* btrow = as_const(a.bt) + static_cast<size_t>(s) * a.MB;
+        WaveState<D> st;
+        st.m = -INFINITY;
+        st.l = 0.0f;
+#pragma unroll
+        for (int J = 0; J < NJ; ++J) st.acc[J] = f4{0, 0, 0, 0};
+        int seg0 = j0;                            // first block of the open piece
+        int cut = min(j1, (j0 / P + 1) * P);      // block after the open piece
+        attend_run<D>(st, btrow, j0, j1, L, a.kc, a.vc, a.Hkv, a.num_blocks, kvh, loff, kg, qB,
+                      ident, a.scale_log2, [&](int j) {
+            if (j + 1 != cut) return;
+            const int part = seg0 / P;
+            const float l_run = sum_over_kg(st.l);
+            const float inv = (l_run > 0.0f) ? 1.0f / l_run : 0.0f;
+            const bool whole = (seg0 == part * P) && (cut == min(nb, (part + 1) * P));
+            // Wave-uniform bases plus lane byte offsets computed here from
+            // the lane index, so no lane address stays live across the block
+            // loop (the kernel runs at its 168-register cap).
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+            const int rr = ln & 15;
+            const int kk = ln >> 4;
+            const size_t row0 = static_cast<size_t>(s) * a.H + h0;
+            if (whole && nparts == 1) {
+                char* ob = pinned_sgpr(reinterpret_cast<char*>(a.out + row0 * D));
+                const unsigned lo = static_cast<unsigned>(rr * D + 4 * kk) * sizeof(f16);
+                if (r < gn) {
+#pragma unroll
+                    for (int J = 0; J < NJ; ++J) {
+                        h4 o;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) o[i] = static_cast<f16>(st.acc[J][i] * inv);
+                        *reinterpret_cast<h4*>(ob + lo + 32u * J) = o;
+                    }
+                }
+            } else if (seg0 == part * P) {
+                const size_t p0 = row0 * a.MP + part;
+                char* ob = pinned_sgpr(reinterpret_cast<char*>(a.ws_out + p0 * D));
+                const unsigned lr = static_cast<unsigned>(rr * a.MP) * sizeof(float);
+                const unsigned lo = lr * D + 16u * kk;
+                if (r < gn) {
+#pragma unroll
+                    for (int J = 0; J < NJ; ++J) {
+                        __builtin_nontemporal_store(st.acc[J] * inv, reinterpret_cast<f4*>(ob + lo + 64u * J));
+                    }
+                    if (kk == 0) {
+                        *reinterpret_cast<float*>(pinned_sgpr(reinterpret_cast<char*>(a.ws_max + p0)) + lr) = st.m;
+                        *reinterpret_cast<float*>(pinned_sgpr(reinterpret_cast<char*>(a.ws_sum + p0)) + lr) = l_run;
+                    }
+                }
+            } else {
+                // The piece after a range boundary: only a wave's first piece
+                // can start inside a partition.
+                char* f = pinned_sgpr(reinterpret_cast<char*>(a.frag + static_cast<size_t>(w) * (kFragHead + gstride * D)));
+                const unsigned lo = static_cast<unsigned>(kFragHead + rr * D + 4 * kk) * sizeof(float);
+                if (r < gn) {
+#pragma unroll
+                    for (int J = 0; J < NJ; ++J) {
+                        __builtin_nontemporal_store(st.acc[J] * inv, reinterpret_cast<f4*>(f + lo + 64u * J));
+                    }
+                    if (kk == 0) {
+                        *reinterpret_cast<float*>(f + 4u * rr) = st.m;
+                        *reinterpret_cast<float*>(f + 4u * (16 + rr)) = l_run;
+                    }
+                }
+            }
+            // The compiler treats the wave's memory counter as out of order
+            // while stores and loads are both in flight, and then waits for
+            // every load before each block: a full wait here, once per
+            // partition, keeps the waits in the block loop exact.
+            wait_vm<0>();
+            st.m = -INFINITY;
+            st.l = 0.0f;
+#pragma unroll
+            for (int J = 0; J < NJ; ++J) st.acc[J] = f4{0, 0, 0, 0};
+            seg0 = cut;
+            cut = min(j1, cut + P);
+        });
+        u = pre + j1;
+    }
+}
+
+// Reduce of the partition streams: one (query head, sequence) combines its
+// nparts partition slots and the boundary slots of teams ta .. tb whose
+// boundary falls strictly inside the sequence's blocks. A boundary at a
+// partition start splits nothing; its fragment is given weight 0 (and the
+// partition slot 0 row, which is finite, as its row).
+struct PStreamReduceArgs {
+    f16* out;
+    const float* ws_max;
+    const float* ws_sum;
+    const float* ws_out;
+    const float* frag;
+    const int* meta;
+    int H, G, nhc, MP, part_blocks, gstride, TS;
+};
+
+template <int D, bool WAVE>
+__device__ __forceinline__ void pstream_reduce_head(const PStreamReduceArgs& a, int s, int h) {
+    const int q = a.meta[0];
+    const int pre = a.meta[2 + s];
+    const int nb = a.meta[3 + s] - pre;
+    const int P = a.part_blocks;
+    const int nparts = (nb + P - 1) / P;
+    // Boundaries t*q strictly inside (pre, pre + nb). When q and pre are
+    // multiples of P every boundary falls on a partition start and splits
+    // nothing, so none is combined.
+    const int ta = pre / q + 1;
+    const int tb = nb > 0 ? (pre + nb - 1) / q : ta - 1;
+    const bool on_starts = (q % P == 0) && (pre % P == 0);
+    const int nbound = on_starts ? 0 : max(0, tb - ta + 1);
+    if (nb == 0 || (nparts == 1 && nbound == 0)) return;  // zeros or written directly
+    const int kvh = h / a.G;
+    const int gk = h - kvh * a.G;
+    const int hc = gk / 16;
+    const int g = gk - hc * 16;
+    const int member = kvh * a.nhc + hc;
+    const size_t row = static_cast<size_t>(s) * a.H + h;
+    const float* pm = a.ws_max + row * a.MP;
+    const float* pl = a.ws_sum + row * a.MP;
+    const float* po = a.ws_out + row * a.MP * D;
+    const size_t fs = kFragHead + static_cast<size_t>(a.gstride) * D;
+    auto split = [&](int i) {  // boundary fragment i: a piece of its own?
+        const int t = ta + i;
+        return (t * q - pre) % P != 0;
+    };
+    auto frag_of = [&](int i) { return a.frag + static_cast<size_t>((ta + i) * a.TS + member) * fs; };
+    auto fm = [&](int p) {
+        if (p < nparts) return pm[p];
+        const int i = p - nparts;
+        return split(i) ? frag_of(i)[g] : -INFINITY;
+    };
+    auto fl = [&](int p) {
+        if (p < nparts) return pl[p];
+        const int i = p - nparts;
+        return split(i) ? frag_of(i)[16 + g] : 0.0f;
+    };
+    auto fo = [&](int p) {
+        if (p < nparts) return po + static_cast<size_t>(p) * D;
+        const int i = p - nparts;
+        return split(i) ? frag_of(i) + kFragHead + static_cast<size_t>(g) * D : po;
+    };
+    f16* o = a.out + row * D;
+    auto out = [&](int d, float v) { o[d] = static_cast<f16>(v); };
+    if constexpr (WAVE) {
+        combine_head_wave<D>(nparts + nbound, fm, fl, fo, out);
+    } else {
+        combine_head<D>(nparts + nbound, fm, fl, fo, out);
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void paged_reduce_pstream_wave_kernel(const PStreamReduceArgs a) {
+    const int h = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (h >= a.H) return;
+    pstream_reduce_head<D, true>(a, blockIdx.y, h);
+}
+
+template <int D>
+__global__ __launch_bounds__(kReduceThreads) void paged_reduce_pstream_kernel(const PStreamReduceArgs a) {
+    pstream_reduce_head<D, false>(a, blockIdx.y, blockIdx.x);
+}
+
 // Bit-exact materialisation of one (sequence, kv head) through the tile
 // addressing above.
 struct GatherArgs {
@@ -1117,21 +1458,45 @@ int decode_v1(void* out, const void* q, const void* kc, const void* vc, const in
     return launched(launch_decode<kWavesV1>(a, sh.D, sh.S, 1, stream), who);
 }
 
+constexpr int kPStreamWavesPerCU = 4 * kPStreamWavesPerSimd;
+
 // Split-K workspace: max logits and exp sums [S][H][MP] and partial outputs
-// [S][H][MP][D], all fp32. Plain scratch: every value a call reads was
-// written earlier in the same call, so it needs no initialisation.
+// [S][H][MP][D], all fp32; with partition streams also the boundary pieces
+// [W][kFragHead + gstride * D] and the team metadata (q, teams, block
+// prefix [S + 1]). Plain scratch: every value a call reads was written
+// earlier in the same call, so it needs no initialisation.
 struct V2Need {
     int MP;          // partitions per sequence
     size_t stat;     // bytes of one [S][H][MP] float array
+    bool pstream;    // partition streams
+    int W;           // waves of the partition-stream grid
+    size_t frag;     // offset of the boundary pieces
+    size_t meta;     // offset of the team metadata
     size_t total;    // bytes of the whole workspace
 };
 
-V2Need v2_need(const Shape& sh, int partition_size) {
+V2Need v2_need(const Shape& sh, int partition_size, int cus) {
     V2Need n{};
     const int part_blocks = partition_size / kBlockTokens;
     n.MP = sh.MB == 0 ? 1 : (sh.MB + part_blocks - 1) / part_blocks;
     n.stat = align_up(sizeof(float) * static_cast<size_t>(sh.S) * sh.H * n.MP);
     n.total = 2 * n.stat + align_up(sizeof(float) * static_cast<size_t>(sh.S) * sh.H * n.MP * sh.D);
+    const int G = sh.H / sh.Hkv;
+    const long long TS = static_cast<long long>(sh.Hkv) * ((G + 15) / 16);
+    n.W = cus * kPStreamWavesPerCU;
+    // Partition streams when partitions are short and the batch has at most
+    // a quarter as many sequences as the grid has teams (a wave then starts
+    // few new sequences, each a pipeline restart), and the lane offsets of
+    // a wave's partial rows fit in 31 bits.
+    const long long teams = TS > 0 ? n.W / TS : 0;
+    n.pstream = sh.S <= kStreamMaxSeqs && part_blocks <= kPStreamMaxPartBlocks && TS > 0 && TS <= n.W &&
+                4LL * sh.S <= teams && 64LL * n.MP * sh.D < (1LL << 31);
+    if (n.pstream) {
+        const size_t gstride = static_cast<size_t>(std::min(16, G));
+        n.frag = n.total;
+        n.meta = n.frag + align_up(sizeof(float) * static_cast<size_t>(n.W) * (kFragHead + gstride * sh.D));
+        n.total = n.meta + align_up(sizeof(int) * (static_cast<size_t>(sh.S) + 3));
+    }
     return n;
 }
 
@@ -1255,7 +1620,47 @@ int effective_partition(const Shape& sh, int partition_size, int cus) {
 
 // Workspace bytes a v2 call with this (effective) partition size uses.
 size_t v2_bytes(const Shape& sh, int partition_size, int cus) {
-    return partition_size == 0 ? stream_need(sh, cus).total : v2_need(sh, partition_size).total;
+    return partition_size == 0 ? stream_need(sh, cus).total : v2_need(sh, partition_size, cus).total;
+}
+
+// Partition streams, then their reduce (which also combines a partition
+// split by a range boundary when the sequence has one partition).
+int decode_pstream(DecodeArgs& a, char* base, const V2Need& need, const Shape& sh,
+                   hipStream_t stream, const char* who) {
+    a.frag = reinterpret_cast<float*>(base + need.frag);
+    a.meta = reinterpret_cast<int*>(base + need.meta);
+    a.W = need.W;
+    const size_t lds = sizeof(int) * (2 * static_cast<size_t>(sh.S) + 1);
+    const dim3 grid(need.W / kStreamWaves);
+    hipError_t err = sh.D == 128
+        ? launch(paged_partition_stream_kernel<128>, grid, dim3(64 * kStreamWaves), lds, stream, a)
+        : launch(paged_partition_stream_kernel<64>, grid, dim3(64 * kStreamWaves), lds, stream, a);
+    if (err != hipSuccess) return launched(err, who);
+    PStreamReduceArgs r{};
+    r.out = a.out;
+    r.ws_max = a.ws_max;
+    r.ws_sum = a.ws_sum;
+    r.ws_out = a.ws_out;
+    r.frag = a.frag;
+    r.meta = a.meta;
+    r.H = a.H;
+    r.G = a.G;
+    r.nhc = a.nhc;
+    r.MP = a.MP;
+    r.part_blocks = a.part_blocks;
+    r.gstride = std::min(16, a.G);
+    r.TS = a.Hkv * a.nhc;
+    if (a.MP <= kWaveReduceMaxParts) {
+        const dim3 rgrid((a.H + 3) / 4, sh.S);
+        err = sh.D == 128 ? launch(paged_reduce_pstream_wave_kernel<128>, rgrid, dim3(256), 0, stream, r)
+                          : launch(paged_reduce_pstream_wave_kernel<64>, rgrid, dim3(256), 0, stream, r);
+    } else {
+        const dim3 rgrid(a.H, sh.S);
+        err = sh.D == 128
+            ? launch(paged_reduce_pstream_kernel<128>, rgrid, dim3(kReduceThreads), 0, stream, r)
+            : launch(paged_reduce_pstream_kernel<64>, rgrid, dim3(kReduceThreads), 0, stream, r);
+    }
+    return launched(err, who);
 }
 
 int decode_v2(void* out, void* ws, size_t ws_bytes, const void* q, const void* kc, const void* vc,
@@ -1273,7 +1678,7 @@ int decode_v2(void* out, void* ws, size_t ws_bytes, const void* q, const void* k
         if (sh.S == 0) return ok();
         return decode_balanced(out, ws, ws_bytes, q, kc, vc, bt, ctx, scale, sh, num_blocks, stream, who);
     }
-    const V2Need need = v2_need(sh, partition_size);
+    const V2Need need = v2_need(sh, partition_size, device_cus());
     if (sh.S > 0) {
         if (ws == nullptr || !aligned(ws, 256)) {
             return fail(SWIFTLLM_ERR_INVALID_PARAMETER, "%s: workspace null or not 256-byte aligned", who);
@@ -1292,6 +1697,7 @@ int decode_v2(void* out, void* ws, size_t ws_bytes, const void* q, const void* k
     a.ws_out = reinterpret_cast<float*>(base + 2 * need.stat);
     a.part_blocks = partition_size / kBlockTokens;
     a.MP = need.MP;
+    if (need.pstream) return decode_pstream(a, base, need, sh, stream, who);
     bool too_large = false;
     hipError_t err = launch_partition<kWavesV2>(a, sh.D, stream, &too_large);
     if (too_large) {
@@ -1464,9 +1870,11 @@ size_t swiftllm_hip_paged_attention_v2_workspace_size(int num_seqs, int num_head
         int n = 0;
         const int cus = (hipGetDeviceCount(&n) == hipSuccess && n > 0) ? device_cus() : kDefaultCUs;
         // the balanced workspace also covers its partitioned fallback
-        return std::max(stream_need(sh, cus).total, v2_need(sh, 512).total);
+        return std::max(stream_need(sh, cus).total, v2_need(sh, 512, cus).total);
     }
-    return v2_need(sh, partition_size).total;
+    int n = 0;
+    const int cus = (hipGetDeviceCount(&n) == hipSuccess && n > 0) ? device_cus() : kDefaultCUs;
+    return v2_need(sh, partition_size, cus).total;
 }
 
 int swiftllm_hip_workspace_clear(void* workspace, size_t bytes, hipStream_t stream) {

@@ -411,3 +411,26 @@ def test_partition_items_longest_first_cover_every_partition(dev, S, ps):
     live = lens > 0
     assert np.all(out[~live] == 0), "empty sequences must be zero"
     assert_attention_close(out[live], _ref(w)[live], f"{S} ragged seqs ps={ps}")
+
+
+@pytest.mark.parametrize("H,Hkv,D", [(64, 8, 128), (64, 2, 128), (32, 8, 64)])
+def test_partition_streams_ragged(dev, H, Hkv, D):
+    """Split-K over short partitions of a batch with few sequences runs as
+    partition streams: equal block ranges per team of waves, cut at partition
+    ends and at range boundaries. Ragged contexts with empty sequences put
+    range boundaries inside partitions, at partition starts and at sequence
+    starts; 16-token partitions make every block a partition, and the 2-kv-head
+    layout (G = 32, two head chunks) gives small teams whose ranges are
+    shorter than a partition."""
+    rng = np.random.default_rng(H + Hkv + D)
+    S = 40
+    lens = np.clip(np.rint(np.exp(rng.normal(np.log(1500.0), 1.2, size=S))), 1, 20000).astype(np.int64)
+    lens[rng.choice(S, size=5, replace=False)] = 0
+    w = _random_batch(rng, lens, H=H, Hkv=Hkv, D=D)
+    dw = DeviceWorkload(w)
+    ref = _ref(w)
+    live = lens > 0
+    for ps in (16, 256, 512, 1024):
+        out = dw.run("v2", partition_size=ps)
+        assert np.all(out[~live] == 0), f"ps={ps}: empty sequences must be zero"
+        assert_attention_close(out[live], ref[live], f"streams H{H} Hkv{Hkv} D{D} ps={ps}")
