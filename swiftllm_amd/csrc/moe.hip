@@ -10,13 +10,14 @@
 // route:    one thread per token; K argmax passes over the E logits (value
 //           descending, ties to the lower index), then weights
 //           w_k = exp(x_k - x_max) / sum_k' exp(x_k' - x_max), which equals the
-//           softmax probabilities renormalised over the selected experts. The
-//           few exponentials per token run in fp64. Rows of up to 16 logits
-//           are loaded into registers at once.
+//           softmax probabilities renormalised over the selected experts, in
+//           fp32. Rows of up to 8 or 16 logits are loaded into registers at
+//           once.
 // dispatch: two kernels, with no grid-wide synchronisation inside either.
 //           (1) rank: one wave per 64-token chunk ranks the chunk's entries
-//               among equal experts with ballots (stable (t, k) order) and
-//               stores per-(chunk, expert) counts. The fused entry point routes
+//               among equal experts with ballots (stable (t, k) order; for up
+//               to 16 experts one unrolled pass of ballots and mbcnt per
+//               expert) and stores per-(chunk, expert) counts. The fused entry point routes
 //               the chunk's tokens first, in the same wave.
 //           (2) permute: each workgroup scans the chunk counts (up to 4096
 //               of them) in LDS into per-(chunk, expert) prefixes and expert
@@ -53,7 +54,8 @@ struct RouteArgs {
     int E;
 };
 
-constexpr int kRouteRegs = 16;  // rows up to this many experts are held in registers
+// Rows of up to R experts (8 or 16) are held in registers: the route and rank
+// kernels are instantiated for both, and wider rows take the loop over memory.
 
 // One argmax pass of the top-K selection: the largest logit among experts
 // not yet taken; the strict '>' keeps the lowest index among equal logits.
@@ -69,51 +71,59 @@ __device__ __forceinline__ void consider(int e, float x, int k, const int (&bi)[
     }
 }
 
-// Writes ids and weights w_k = exp(x_k - x_0) / sum_k' exp(x_k' - x_0) of token t.
+// Writes ids and weights w_k = exp(x_k - x_0) / sum_k' exp(x_k' - x_0) of token t,
+// in fp32: every exponent is <= 0 and the sum lies in [1, K], so the weights
+// are within a few fp32 ulps (under 1e-6) of the fp64 values.
 template <int K>
 __device__ __forceinline__ void write_route(const RouteArgs& a, int t, const float (&bv)[K],
                                             const int (&bi)[K]) {
-    double ex[K];
-    double sum = 0.0;
+    float ex[K];
+    float sum = 0.0f;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-        ex[k] = exp(static_cast<double>(bv[k]) - static_cast<double>(bv[0]));
+        ex[k] = expf(bv[k] - bv[0]);
         sum += ex[k];
     }
 #pragma unroll
     for (int k = 0; k < K; ++k) {
         a.ids[static_cast<size_t>(t) * K + k] = bi[k];
-        a.w[static_cast<size_t>(t) * K + k] = static_cast<float>(ex[k] / sum);
+        a.w[static_cast<size_t>(t) * K + k] = ex[k] / sum;
     }
 }
 
 // Top-K of one row of logits into bv (values) and bi (expert ids).
-template <int K>
+template <int K, int R>
 __device__ __forceinline__ void select_topk(const float* row, int E, float (&bv)[K], int (&bi)[K]) {
+    static_assert(R == 8 || R == 16, "register row width");
 #pragma unroll
     for (int k = 0; k < K; ++k) bi[k] = -1;
-    if (E <= kRouteRegs) {
+    if (E <= R) {
         // All loads issued together (16-byte loads when the row allows); the K
         // passes then run on registers.
-        float v[kRouteRegs];
+        float v[R];
         if ((E & 3) == 0 && (reinterpret_cast<uintptr_t>(row) & 15) == 0) {
             typedef float f4v __attribute__((ext_vector_type(4)));
+            // Every load is issued, the ones past the row re-reading its
+            // first 16 bytes, so no branch separates them and one wait
+            // covers all.
+            f4v x[R / 4];
 #pragma unroll
-            for (int q = 0; q < kRouteRegs / 4; ++q) {
-                const f4v x = (4 * q < E) ? reinterpret_cast<const f4v*>(row)[q] : f4v{0, 0, 0, 0};
+            for (int q = 0; q < R / 4; ++q) x[q] = reinterpret_cast<const f4v*>(row)[4 * q < E ? q : 0];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) v[4 * q + i] = x[i];
+            for (int q = 0; q < R / 4; ++q) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[4 * q + i] = (4 * q < E) ? x[q][i] : 0.0f;
             }
         } else {
 #pragma unroll
-            for (int e = 0; e < kRouteRegs; ++e) v[e] = (e < E) ? row[e] : 0.0f;
+            for (int e = 0; e < R; ++e) v[e] = (e < E) ? row[e] : 0.0f;
         }
 #pragma unroll
         for (int k = 0; k < K; ++k) {
             float best = 0.0f;
             int besti = -1;
 #pragma unroll
-            for (int e = 0; e < kRouteRegs; ++e) {
+            for (int e = 0; e < R; ++e) {
                 if (e < E) consider<K>(e, v[e], k, bi, best, besti);
             }
             bv[k] = best;
@@ -131,13 +141,13 @@ __device__ __forceinline__ void select_topk(const float* row, int E, float (&bv)
     }
 }
 
-template <int K>
+template <int K, int R>
 __global__ __launch_bounds__(256) void moe_route_kernel(const RouteArgs a) {
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= a.T) return;
     float bv[K];
     int bi[K];
-    select_topk<K>(a.logits + static_cast<size_t>(t) * a.E, a.E, bv, bi);
+    select_topk<K, R>(a.logits + static_cast<size_t>(t) * a.E, a.E, bv, bi);
     write_route<K>(a, t, bv, bi);
 }
 
@@ -187,6 +197,47 @@ __device__ __forceinline__ void rank_chunk(const int (&id)[K], int (&rk)[K], int
     }
 }
 
+// rank_chunk for E <= kRankUnrolled, with no loop-carried branch: for each
+// expert e, K ballots give the chunk's entries of e per top-k slot, and
+// mbcnt counts those below the lane. An entry (t, k) of expert e ranks after
+// every entry of e at a lower token (any slot) and after the token's own
+// slots k' < k holding e. Lane e < E returns expert e's count in `cnt`.
+constexpr int kRankUnrolled = 16;
+
+template <int K>
+__device__ __forceinline__ void rank_chunk_unrolled(const int (&id)[K], int (&rk)[K], int E, int lane,
+                                                    int& cnt) {
+    bool ok[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        ok[k] = id[k] >= 0 && id[k] < E;
+        rk[k] = -1;
+    }
+    cnt = 0;
+#pragma unroll
+    for (int e = 0; e < kRankUnrolled; ++e) {
+        if (e < E) {  // wave-uniform
+            int below = 0, total = 0;
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+                const unsigned long long m = __ballot(ok[k] && id[k] == e);
+                below += __builtin_amdgcn_mbcnt_hi(static_cast<unsigned>(m >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(m), 0u));
+                total += __popcll(m);
+            }
+            int own = 0;
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+                if (ok[k] && id[k] == e) {
+                    rk[k] = below + own;
+                    ++own;
+                }
+            }
+            if (lane == e) cnt = total;
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // (1) Rank, optionally after routing.
 // ---------------------------------------------------------------------------
@@ -203,14 +254,16 @@ struct RankArgs {
 
 constexpr int kRankWaves = 4;
 
-template <int K>
+template <int K, int R>
 __global__ __launch_bounds__(64 * kRankWaves) void moe_rank_kernel(const RankArgs a) {
     __shared__ int s_cnt[kRankWaves][kMaxExperts];
     const int lane = threadIdx.x & 63;
     const int wv = threadIdx.x >> 6;
     const int c = blockIdx.x * kRankWaves + wv;  // chunk of this wave
     if (c >= a.nchunks) return;                   // whole waves only; no barriers below
-    for (int e = lane; e < a.E; e += 64) s_cnt[wv][e] = 0;
+    if (a.E > kRankUnrolled) {
+        for (int e = lane; e < a.E; e += 64) s_cnt[wv][e] = 0;
+    }
 
     const int t = c * kChunkTokens + lane;
     const bool live = t < a.T;
@@ -218,7 +271,7 @@ __global__ __launch_bounds__(64 * kRankWaves) void moe_rank_kernel(const RankArg
     if (a.logits != nullptr) {
         float bv[K];
         if (live) {
-            select_topk<K>(a.logits + static_cast<size_t>(t) * a.E, a.E, bv, id);
+            select_topk<K, R>(a.logits + static_cast<size_t>(t) * a.E, a.E, bv, id);
             RouteArgs ra{a.logits, a.ids, a.w, a.T, a.E};
             write_route<K>(ra, t, bv, id);
         } else {
@@ -228,6 +281,16 @@ __global__ __launch_bounds__(64 * kRankWaves) void moe_rank_kernel(const RankArg
     } else {
 #pragma unroll
         for (int k = 0; k < K; ++k) id[k] = live ? a.ids[static_cast<size_t>(t) * K + k] : -1;
+    }
+    if (a.E <= kRankUnrolled) {
+        int cnt;
+        rank_chunk_unrolled<K>(id, rk, a.E, lane, cnt);
+        if (live) {
+#pragma unroll
+            for (int k = 0; k < K; ++k) a.rank[static_cast<size_t>(t) * K + k] = rk[k];
+        }
+        if (lane < a.E) a.cnt[static_cast<size_t>(c) * a.E + lane] = cnt;
+        return;
     }
     rank_chunk<K>(id, rk, a.E, lane, s_cnt[wv]);
     if (live) {
@@ -310,34 +373,63 @@ struct PermuteArgs {
     int vec;  // 1: rows move as 16-byte vectors
 };
 
-template <int K>
+// VEC: rows move as 16-byte vectors (a.xp set and a.vec); otherwise index
+// arrays only, or a 2-byte copy of unaligned rows.
+template <int K, bool VEC>
 __global__ __launch_bounds__(64 * kPermuteWaves) void moe_permute_kernel(const PermuteArgs a) {
     __shared__ int s_base[kLdsCounts];  // [nchunks][E] exclusive prefixes over chunks
     __shared__ int s_off[kMaxExperts];  // expert offsets
+    if (a.T == 0) {
+        // No tokens (one workgroup): zero counts and offsets. Below, T >= 1,
+        // so the clamped indices of the preloads are valid.
+        for (int e = threadIdx.x; e < a.E; e += blockDim.x) a.counts[e] = 0;
+        for (int e = threadIdx.x; e <= a.E; e += blockDim.x) a.offsets[e] = 0;
+        return;
+    }
     const int lane = threadIdx.x & 63;
     const int wv = threadIdx.x >> 6;
     const int t = blockIdx.x * kPermuteWaves + wv;
     const bool live = t < a.T;
-    const bool copy = live && a.xp != nullptr && a.vec;
     const int nv = a.hidden / 8;
     const u32x4* __restrict__ src =
-        reinterpret_cast<const u32x4*>(a.x + static_cast<size_t>(live ? t : 0) * a.hidden);
+        reinterpret_cast<const u32x4*>(a.x + static_cast<size_t>(min(t, a.T - 1)) * a.hidden);
 
-    // The first batch of the row is loaded before the bookkeeping below, so
-    // its latency hides the scans.
-    u32x4 v[kCopyBatch];
-    if (copy) {
+    // Loads in the order their values are needed, since the memory counter
+    // completes in order: the chunk counts (scanned first), the token's expert
+    // ids and ranks, then the first batch of the row, whose latency hides the
+    // scans. Every load is issued unconditionally (out-of-range ones re-read a
+    // valid element and are discarded), so no branch merge makes the compiler
+    // wait for all of them before the first count is used.
+    constexpr int kCntPerThread = kLdsCounts / (64 * kPermuteWaves);
+    const int n = a.nchunks * a.E;
+    int cv[kCntPerThread];
+    if (a.base == nullptr) {
 #pragma unroll
-        for (int u = 0; u < kCopyBatch; ++u) {
-            const int i = 64 * u + lane;
-            if (i < nv) v[u] = src[i];
+        for (int j = 0; j < kCntPerThread; ++j) {
+            const int i = threadIdx.x + 64 * kPermuteWaves * j;
+            cv[j] = a.cnt[min(i, n - 1)];
         }
+    }
+    const int tc = min(t, a.T - 1);
+    int eid[K], erk[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        eid[k] = a.ids[static_cast<size_t>(tc) * K + k];
+        erk[k] = a.rank[static_cast<size_t>(tc) * K + k];
+    }
+    u32x4 v[kCopyBatch];
+    if constexpr (VEC) {
+#pragma unroll
+        for (int u = 0; u < kCopyBatch; ++u) v[u] = src[min(64 * u + lane, nv - 1)];
     }
 
     // Per-expert totals: from the scan kernel, or scanned here from the counts.
     if (a.base == nullptr) {
-        const int n = a.nchunks * a.E;
-        for (int i = threadIdx.x; i < n; i += 64 * kPermuteWaves) s_base[i] = a.cnt[i];
+#pragma unroll
+        for (int j = 0; j < kCntPerThread; ++j) {
+            const int i = threadIdx.x + 64 * kPermuteWaves * j;
+            if (i < n) s_base[i] = cv[j];
+        }
         __syncthreads();
         // One wave per expert column, 64 chunks per step.
         for (int e = wv; e < a.E; e += kPermuteWaves) {
@@ -381,8 +473,8 @@ __global__ __launch_bounds__(64 * kPermuteWaves) void moe_permute_kernel(const P
     long long rows[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-        const int e = a.ids[static_cast<size_t>(t) * K + k];
-        const int rk = a.rank[static_cast<size_t>(t) * K + k];
+        const int e = eid[k];
+        const int rk = erk[k];
         int row = -1;
         if (e >= 0 && e < a.E && rk >= 0) {
             const size_t ce = static_cast<size_t>(c) * a.E + e;
@@ -395,7 +487,7 @@ __global__ __launch_bounds__(64 * kPermuteWaves) void moe_permute_kernel(const P
         }
     }
     if (a.xp == nullptr) return;
-    if (a.vec) {
+    if constexpr (VEC) {
         for (int i0 = 0; i0 < nv; i0 += 64 * kCopyBatch) {
             if (i0 > 0) {
 #pragma unroll
@@ -444,7 +536,8 @@ hipError_t by_k(int K, Args&&... args) {
 template <int K>
 struct RouteLaunch {
     static hipError_t run(const RouteArgs& a, hipStream_t s) {
-        return launch(moe_route_kernel<K>, dim3((a.T + 255) / 256), dim3(256), 0, s, a);
+        if (a.E <= 8) return launch(moe_route_kernel<K, 8>, dim3((a.T + 255) / 256), dim3(256), 0, s, a);
+        return launch(moe_route_kernel<K, 16>, dim3((a.T + 255) / 256), dim3(256), 0, s, a);
     }
 };
 
@@ -452,7 +545,8 @@ template <int K>
 struct RankLaunch {
     static hipError_t run(const RankArgs& a, hipStream_t s) {
         const int grid = (a.nchunks + kRankWaves - 1) / kRankWaves;
-        return launch(moe_rank_kernel<K>, dim3(grid), dim3(64 * kRankWaves), 0, s, a);
+        if (a.E <= 8) return launch(moe_rank_kernel<K, 8>, dim3(grid), dim3(64 * kRankWaves), 0, s, a);
+        return launch(moe_rank_kernel<K, 16>, dim3(grid), dim3(64 * kRankWaves), 0, s, a);
     }
 };
 
@@ -462,7 +556,10 @@ struct PermuteLaunch {
         // One wave per token; at least one workgroup so counts and offsets
         // are written when there are no tokens.
         const int grid = a.T > 0 ? (a.T + kPermuteWaves - 1) / kPermuteWaves : 1;
-        return launch(moe_permute_kernel<K>, dim3(grid), dim3(64 * kPermuteWaves), 0, s, a);
+        if (a.xp != nullptr && a.vec) {
+            return launch(moe_permute_kernel<K, true>, dim3(grid), dim3(64 * kPermuteWaves), 0, s, a);
+        }
+        return launch(moe_permute_kernel<K, false>, dim3(grid), dim3(64 * kPermuteWaves), 0, s, a);
     }
 };
 
