@@ -1,5 +1,6 @@
 """The hot path inside a HIP graph: a ragged decode step (cache write, then
-single-pass and balanced decode), the fused MoE route + dispatch, and the
+single-pass, balanced and 512-token split-K decode, the last as partition
+streams at this batch size), the fused MoE route + dispatch, and the
 whole MoE layer (MoeMlp.forward: dispatch, expert GEMMs with their thin
 tails, combine) are captured once and replayed several times, with new inputs uploaded and the
 program's own eager work and synchronisation between replays; every replay
@@ -35,10 +36,15 @@ class _Step:
         self.slots = DeviceArray.from_numpy(w.slot_mapping)
         self.o1 = DeviceArray(w.q.shape, np.float16)
         self.o2 = DeviceArray(w.q.shape, np.float16)
+        self.o3 = DeviceArray(w.q.shape, np.float16)
         need = pa.paged_attention_v2_workspace_size(sh["num_seqs"], sh["num_heads"],
                                                     sh["num_kv_heads"], sh["head_dim"], 16,
                                                     sh["max_num_blocks_per_seq"], 0)
         self.ws = DeviceArray((need // 4 + 1,), np.uint32)
+        need = pa.paged_attention_v2_workspace_size(sh["num_seqs"], sh["num_heads"],
+                                                    sh["num_kv_heads"], sh["head_dim"], 16,
+                                                    sh["max_num_blocks_per_seq"], 512)
+        self.ws3 = DeviceArray((need // 4 + 1,), np.uint32)
 
     def enqueue(self, stream):
         w, sh = self.w, self.sh
@@ -50,6 +56,8 @@ class _Step:
                               Hkv, D, 16, MB, num_blocks=NB, stream=stream)
         pa.paged_attention_v2(self.o2, self.ws, self.q, self.kc, self.vc, self.bt, self.ctx,
                               w.scale, S, H, Hkv, D, 16, MB, 0, num_blocks=NB, stream=stream)
+        pa.paged_attention_v2(self.o3, self.ws3, self.q, self.kc, self.vc, self.bt, self.ctx,
+                              w.scale, S, H, Hkv, D, 16, MB, 512, num_blocks=NB, stream=stream)
 
     def upload(self, rng):
         """New query and new-token K/V (same shapes and slots)."""
@@ -76,13 +84,14 @@ def test_decode_step_graph_replays_match_eager(dev):
         stream.synchronize()
         eager.enqueue(stream)        # eager work between replays
         stream.synchronize()
-        for a, b in ((step.o1, eager.o1), (step.o2, eager.o2)):
+        for a, b in ((step.o1, eager.o1), (step.o2, eager.o2), (step.o3, eager.o3)):
             assert np.array_equal(a.numpy().view(np.uint16), b.numpy().view(np.uint16)), rep
         # and the result is right: the oracle on the cache the step wrote
         kc, vc = step.kc.numpy(), step.vc.numpy()
         ref = oracle.decode_f64(w.q, kc, vc, w.block_tables, w.context_lens, w.scale)
         assert_attention_close(step.o1.numpy(), ref, f"graph replay {rep} v1")
         assert_attention_close(step.o2.numpy(), ref, f"graph replay {rep} balanced")
+        assert_attention_close(step.o3.numpy(), ref, f"graph replay {rep} split-K 512")
 
 
 def test_moe_route_dispatch_graph_replays_match_eager(dev):

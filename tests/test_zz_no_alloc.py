@@ -103,7 +103,8 @@ def test_noalloc_first_call_captured_in_a_graph(dev):
 
 
 def test_noalloc_matches_workspace_entry_on_consecutive_calls(dev):
-    """Config 3's heads at 16384 tokens in 512-token partitions (8.4 MB of
+    """Config 3's heads at 16384 tokens in 512-token partitions (partition
+    streams: 8.4 MB of partial outputs and 8.7 MB of boundary slots in the
     scratch, the workgroup reduce over 32 partitions), then a smaller batch
     (config 1's shape) at 64-token partitions, then the small batch again in
     balanced mode: each bit-equal to the workspace entry point and within the
