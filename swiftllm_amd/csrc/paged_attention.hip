@@ -500,74 +500,15 @@ void paged_partition_kernel(const DecodeArgs a) {
 // Rescaled combine of P fragments of one query head: fragment p holds a max
 // m_p (log2 domain), a sum l_p and a normalised partial output o_p[D], and
 // out[d] = sum_p w_p o_p[d] / sum_p w_p with w_p = exp2(m_p - M) l_p,
-// M = max_p m_p. One workgroup of kReduceThreads threads per head: threads
-// own 4 consecutive outputs (one 16-byte load per fragment) of every PG-th
-// fragment, so PG fragments are in flight per load step, and an LDS pass adds
-// the PG shares. Accessors: fm(p), fl(p) and fo(p) (pointer to o_p, 16-byte
+// M = max_p m_p. Accessors: fm(p), fl(p) and fo(p) (pointer to o_p, 8-byte
 // aligned); out(d, v) stores one output.
-constexpr int kReduceThreads = 256;
-constexpr int kReduceChunk = 1024;  // fragment weights staged in LDS per pass
-
-template <int D, typename FM, typename FL, typename FO, typename OUT>
-__device__ __forceinline__ void combine_head(int P, FM fm, FL fl, FO fo, OUT out) {
-    constexpr int LQ = D / 4;                 // threads per fragment row
-    constexpr int PG = kReduceThreads / LQ;   // fragment shares
-    constexpr int NWV = kReduceThreads / 64;
-    __shared__ float s_w[kReduceChunk];
-    __shared__ float s_red[2][NWV];
-    __shared__ f4 s_acc[kReduceThreads];
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wv = tid >> 6;
-    float m = -INFINITY;
-    for (int p = tid; p < P; p += kReduceThreads) m = fmaxf(m, fm(p));
-    m = wave_max(m);
-    if (lane == 0) s_red[0][wv] = m;
-    __syncthreads();
-    float M = s_red[0][0];
-#pragma unroll
-    for (int i = 1; i < NWV; ++i) M = fmaxf(M, s_red[0][i]);
-    const int share = tid / LQ;
-    const int d4 = (tid - share * LQ) * 4;
-    f4 acc = f4{0, 0, 0, 0};
-    float den = 0.0f;
-    for (int c0 = 0; c0 < P; c0 += kReduceChunk) {
-        const int cn = min(kReduceChunk, P - c0);
-        for (int i = tid; i < cn; i += kReduceThreads) {
-            const float mp = fm(c0 + i);
-            const float w = (mp == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mp - M) * fl(c0 + i);
-            s_w[i] = w;
-            den += w;
-        }
-        __syncthreads();
-#pragma unroll 4
-        for (int i = share; i < cn; i += PG) {
-            acc += s_w[i] * *reinterpret_cast<const f4*>(fo(c0 + i) + d4);
-        }
-        __syncthreads();
-    }
-    den = wave_sum(den);
-    if (lane == 0) s_red[1][wv] = den;
-    s_acc[tid] = acc;
-    __syncthreads();
-    if (tid < LQ) {
-        f4 sum = s_acc[tid];
-#pragma unroll
-        for (int f = 1; f < PG; ++f) sum += s_acc[f * LQ + tid];
-        float dd = 0.0f;
-#pragma unroll
-        for (int i = 0; i < NWV; ++i) dd += s_red[1][i];
-        const float inv = dd > 0.0f ? 1.0f / dd : 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) out(d4 + i, sum[i] * inv);
-    }
-}
-
-// The same combine on one wave, for items with few fragments: no barriers,
-// lane l owns outputs [l * D / 64, (l + 1) * D / 64) (one coalesced row of
-// the fragment per load) and up to 16 fragment loads per lane are in flight.
-// The weights of up to 64 fragments live one per lane and are broadcast with
-// readlane; the first 64 headers are loaded once.
+// The same combine on one wave: no barriers, lane l owns outputs
+// [l * D / 64, (l + 1) * D / 64), so every fragment row is one coalesced load.
+// The rows of the first CH fragments are loaded before the headers (max and
+// sum) of the first 64, all in flight together, so the combine pays one
+// memory latency per CH fragments; rows past the last fragment re-read it
+// and get weight 0. The weights live one per lane and are broadcast with
+// readlane; the rows are added in fragment order.
 template <int D>
 __device__ __forceinline__ void load_row(const float* p, float (&v)[D / 64]) {
     if constexpr (D == 128) {
@@ -583,10 +524,19 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 
-template <int D, typename FM, typename FL, typename FO, typename OUT>
+template <int D, int CH, typename FM, typename FL, typename FO, typename OUT>
 __device__ __forceinline__ void combine_head_wave(int P, FM fm, FL fl, FO fo, OUT out) {
+    static_assert(CH == 16 || CH == 64, "rows per load batch");
     constexpr int DL = D / 64;
     const int lane = threadIdx.x & 63;
+    if (P <= 0) {
+#pragma unroll
+        for (int j = 0; j < DL; ++j) out(lane * DL + j, 0.0f);
+        return;
+    }
+    float v[CH][DL];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) load_row<D>(fo(min(i, P - 1)) + lane * DL, v[i]);
     const float m0 = lane < P ? fm(lane) : -INFINITY;
     const float l0 = lane < P ? fl(lane) : 0.0f;
     float M = m0;
@@ -596,29 +546,28 @@ __device__ __forceinline__ void combine_head_wave(int P, FM fm, FL fl, FO fo, OU
 #pragma unroll
     for (int j = 0; j < DL; ++j) acc[j] = 0.0f;
     float den = 0.0f;
-    for (int c0 = 0; c0 < P; c0 += 64) {
-        float w;
-        if (c0 == 0) {
-            w = (m0 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m0 - M) * l0;
-        } else {
-            const int p = c0 + lane;
-            const float mp = p < P ? fm(p) : -INFINITY;
-            w = (mp == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mp - M) * fl(p);
-        }
-        den += w;
-        // Batches of 16 unconditional loads: lanes past the last fragment
-        // hold weight 0 and re-read the last fragment instead of branching.
-        const int cn = min(64, P - c0);
-        for (int i0 = 0; i0 < cn; i0 += 16) {
-#pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                const int i = i0 + k;  // < 64: i0 <= 48
-                const float wi = readlane_f(w, i);
-                float v[DL];
-                load_row<D>(fo(min(c0 + i, P - 1)) + lane * DL, v);
-#pragma unroll
-                for (int j = 0; j < DL; ++j) acc[j] += wi * v[j];
+    float w = 0.0f;
+    for (int c0 = 0; c0 < P; c0 += CH) {
+        if ((c0 & 63) == 0) {
+            // Weights of fragments c0 .. c0 + 63, fragment c0 + l on lane l.
+            if (c0 == 0) {
+                w = (m0 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m0 - M) * l0;
+            } else {
+                const int p = c0 + lane;
+                const float mp = p < P ? fm(p) : -INFINITY;
+                w = (mp == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mp - M) * fl(p);
             }
+            den += w;
+        }
+        if (c0 > 0) {
+#pragma unroll
+            for (int i = 0; i < CH; ++i) load_row<D>(fo(min(c0 + i, P - 1)) + lane * DL, v[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const float wi = readlane_f(w, (c0 & 63) + i);
+#pragma unroll
+            for (int j = 0; j < DL; ++j) acc[j] += wi * v[i][j];
         }
     }
     den = wave_sum(den);
@@ -626,6 +575,10 @@ __device__ __forceinline__ void combine_head_wave(int P, FM fm, FL fl, FO fo, OU
 #pragma unroll
     for (int j = 0; j < DL; ++j) out(lane * DL + j, acc[j] * inv);
 }
+
+// Fragment rows per load batch of a head's combine: 16 for up to 16
+// fragments, else 64 (128 registers of rows at D = 128).
+constexpr int kReduceSmall = 16;
 
 // Split-K reduce: one workgroup per (query head, sequence); sequences with a
 // single partition were written directly by the partition kernel.
@@ -641,9 +594,9 @@ struct ReduceArgs {
     int MP;
 };
 
-// Few partitions per sequence: one wave per (query head, sequence), four
-// heads per workgroup.
-template <int D>
+// One wave per (query head, sequence), four heads per workgroup; CH fragment
+// rows per load batch.
+template <int D, int CH>
 __global__ __launch_bounds__(256) void paged_reduce_wave_kernel(const ReduceArgs a) {
     const int h = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int s = blockIdx.y;
@@ -657,30 +610,12 @@ __global__ __launch_bounds__(256) void paged_reduce_wave_kernel(const ReduceArgs
     const float* pl = a.ws_sum + row * a.MP;
     const float* po = a.ws_out + row * a.MP * D;
     f16* o = a.out + row * D;
-    combine_head_wave<D>(
+    combine_head_wave<D, CH>(
         nparts, [&](int p) { return pm[p]; }, [&](int p) { return pl[p]; },
         [&](int p) { return po + static_cast<size_t>(p) * D; },
         [&](int d, float v) { o[d] = static_cast<f16>(v); });
 }
 
-template <int D>
-__global__ __launch_bounds__(kReduceThreads) void paged_reduce_kernel(const ReduceArgs a) {
-    const int h = blockIdx.x;
-    const int s = blockIdx.y;
-    const int L = max(a.ctx[s], 0);
-    const int nblk = min((L + kBlockTokens - 1) / kBlockTokens, a.MB);
-    const int nparts = (nblk + a.part_blocks - 1) / a.part_blocks;
-    if (nparts <= 1) return;
-    const size_t row = static_cast<size_t>(s) * a.H + h;
-    const float* pm = a.ws_max + row * a.MP;
-    const float* pl = a.ws_sum + row * a.MP;
-    const float* po = a.ws_out + row * a.MP * D;
-    f16* o = a.out + row * D;
-    combine_head<D>(
-        nparts, [&](int p) { return pm[p]; }, [&](int p) { return pl[p]; },
-        [&](int p) { return po + static_cast<size_t>(p) * D; },
-        [&](int d, float v) { o[d] = static_cast<f16>(v); });
-}
 
 // ---------------------------------------------------------------------------
 // Balanced ("stream-K") decode. The blocks of all sequences form one list,
@@ -934,7 +869,7 @@ __global__ __launch_bounds__(256) void paged_streamk_reduce_kernel(const StreamR
         return a.frag + slot * fs;
     };
     f16* o = a.out + (static_cast<size_t>(s) * a.H + kvh * a.G + g0 + g) * D;
-    combine_head_wave<D>(
+    combine_head_wave<D, kReduceSmall>(
         P, [&](int i) { return frag_of(i)[g]; }, [&](int i) { return frag_of(i)[16 + g]; },
         [&](int i) { return frag_of(i) + kFragHead + static_cast<size_t>(g) * D; },
         [&](int d, float v) { o[d] = static_cast<f16>(v); });
@@ -1210,7 +1145,7 @@ struct PStreamReduceArgs {
     int H, G, nhc, MP, part_blocks, gstride, TS;
 };
 
-template <int D, bool WAVE>
+template <int D, int CH>
 __device__ __forceinline__ void pstream_reduce_head(const PStreamReduceArgs& a, int s, int h) {
     const int q = a.meta[0];
     const int pre = a.meta[2 + s];
@@ -1257,23 +1192,14 @@ __device__ __forceinline__ void pstream_reduce_head(const PStreamReduceArgs& a, 
     };
     f16* o = a.out + row * D;
     auto out = [&](int d, float v) { o[d] = static_cast<f16>(v); };
-    if constexpr (WAVE) {
-        combine_head_wave<D>(nparts + nbound, fm, fl, fo, out);
-    } else {
-        combine_head<D>(nparts + nbound, fm, fl, fo, out);
-    }
+    combine_head_wave<D, CH>(nparts + nbound, fm, fl, fo, out);
 }
 
-template <int D>
+template <int D, int CH>
 __global__ __launch_bounds__(256) void paged_reduce_pstream_wave_kernel(const PStreamReduceArgs a) {
     const int h = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (h >= a.H) return;
-    pstream_reduce_head<D, true>(a, blockIdx.y, h);
-}
-
-template <int D>
-__global__ __launch_bounds__(kReduceThreads) void paged_reduce_pstream_kernel(const PStreamReduceArgs a) {
-    pstream_reduce_head<D, false>(a, blockIdx.y, blockIdx.x);
+    pstream_reduce_head<D, CH>(a, blockIdx.y, h);
 }
 
 // Bit-exact materialisation of one (sequence, kv head) through the tile
@@ -1500,19 +1426,13 @@ V2Need v2_need(const Shape& sh, int partition_size, int cus) {
     return n;
 }
 
-// Up to kWaveReduceMaxParts partitions per sequence a wave combines a head;
-// more partitions get a workgroup per head.
-#ifndef SWIFTLLM_WAVE_REDUCE_MAX_PARTS
-#define SWIFTLLM_WAVE_REDUCE_MAX_PARTS 16
-#endif
-constexpr int kWaveReduceMaxParts = SWIFTLLM_WAVE_REDUCE_MAX_PARTS;
-
+// A wave combines a head: row batches of kReduceSmall for up to that many
+// partitions per sequence, else of 64.
 template <int D>
 hipError_t launch_reduce_t(const ReduceArgs& r, int S, hipStream_t stream) {
-    if (r.MP <= kWaveReduceMaxParts) {
-        return launch(paged_reduce_wave_kernel<D>, dim3((r.H + 3) / 4, S), dim3(256), 0, stream, r);
-    }
-    return launch(paged_reduce_kernel<D>, dim3(r.H, S), dim3(kReduceThreads), 0, stream, r);
+    const dim3 grid((r.H + 3) / 4, S);
+    if (r.MP <= kReduceSmall) return launch(paged_reduce_wave_kernel<D, kReduceSmall>, grid, dim3(256), 0, stream, r);
+    return launch(paged_reduce_wave_kernel<D, 64>, grid, dim3(256), 0, stream, r);
 }
 
 int validate_partition(const char* who, int partition_size) {
@@ -1650,15 +1570,15 @@ int decode_pstream(DecodeArgs& a, char* base, const V2Need& need, const Shape& s
     r.part_blocks = a.part_blocks;
     r.gstride = std::min(16, a.G);
     r.TS = a.Hkv * a.nhc;
-    if (a.MP <= kWaveReduceMaxParts) {
-        const dim3 rgrid((a.H + 3) / 4, sh.S);
-        err = sh.D == 128 ? launch(paged_reduce_pstream_wave_kernel<128>, rgrid, dim3(256), 0, stream, r)
-                          : launch(paged_reduce_pstream_wave_kernel<64>, rgrid, dim3(256), 0, stream, r);
+    // Partition slots and boundary slots: at most MP + (MP - 1) fragments
+    // per head when every partition holds a boundary.
+    const dim3 rgrid((a.H + 3) / 4, sh.S);
+    if (2 * a.MP - 1 <= kReduceSmall) {
+        err = sh.D == 128 ? launch(paged_reduce_pstream_wave_kernel<128, kReduceSmall>, rgrid, dim3(256), 0, stream, r)
+                          : launch(paged_reduce_pstream_wave_kernel<64, kReduceSmall>, rgrid, dim3(256), 0, stream, r);
     } else {
-        const dim3 rgrid(a.H, sh.S);
-        err = sh.D == 128
-            ? launch(paged_reduce_pstream_kernel<128>, rgrid, dim3(kReduceThreads), 0, stream, r)
-            : launch(paged_reduce_pstream_kernel<64>, rgrid, dim3(kReduceThreads), 0, stream, r);
+        err = sh.D == 128 ? launch(paged_reduce_pstream_wave_kernel<128, 64>, rgrid, dim3(256), 0, stream, r)
+                          : launch(paged_reduce_pstream_wave_kernel<64, 64>, rgrid, dim3(256), 0, stream, r);
     }
     return launched(err, who);
 }
