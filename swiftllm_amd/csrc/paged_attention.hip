@@ -71,6 +71,7 @@ struct DecodeArgs {
     float* frag;      // [W][kFragHead + gstride * D]: the piece a wave's range starts with
     int* meta;        // [0] blocks per team q, [1] teams, [2 .. S + 2] block prefix
     int W;            // waves in the grid
+    int stage_off;    // ints of dynamic LDS before the waves' partial slots
 };
 
 // Attends `count` blocks of one sequence: logical blocks first,
@@ -966,6 +967,45 @@ constexpr int kPStreamWavesPerSimd = SWIFTLLM_PSTREAM_WAVES_PER_SIMD;
 // Teams of a partition-stream grid of W waves, TS waves per team.
 __host__ __device__ __forceinline__ int pstream_teams(int W, int TS) { return max(1, W / TS); }
 
+// Where a piece's partial goes: rows (lane row r at rows + r * rstride, 16
+// bytes per lane group and 16-row slice), max and sum (row r at m / l +
+// r * mstride). Wave-uniform.
+struct PieceDst {
+    char* rows;
+    char* m;
+    char* l;
+    unsigned rstride;
+    unsigned mstride;
+};
+
+// Floats a lane keeps in its LDS slot: its NJ output vectors, max and sum
+// (padded to 16 bytes).
+template <int D>
+constexpr int kStageFloats = 4 * (D / 16) + 4;
+
+// Writes a piece's partial: lane (r, kg) its four outputs of each 16-row
+// slice of row r, lanes with kg = 0 the row's max and sum; rows r >= gn
+// (padding) are skipped. The lane offsets are computed here from the lane
+// index (behind an empty asm), so none stays live in a register.
+template <int D>
+__device__ __forceinline__ void write_piece(const PieceDst& d, int lane, bool row_ok, const f4 (&v)[D / 16],
+                                            float m, float l) {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const unsigned rr = static_cast<unsigned>(ln & 15);
+    const unsigned kk = static_cast<unsigned>(ln >> 4);
+    char* rows = pinned_sgpr(d.rows);
+    if (row_ok) {
+        const unsigned lo = rr * d.rstride + 16u * kk;
+#pragma unroll
+        for (int J = 0; J < D / 16; ++J) __builtin_nontemporal_store(v[J], reinterpret_cast<f4*>(rows + lo + 64u * J));
+        if (kk == 0) {
+            *reinterpret_cast<float*>(pinned_sgpr(d.m) + rr * d.mstride) = m;
+            *reinterpret_cast<float*>(pinned_sgpr(d.l) + rr * d.mstride) = l;
+        }
+    }
+}
+
 template <int D>
 __global__ __launch_bounds__(64 * kStreamWaves) __attribute__((amdgpu_waves_per_eu(kPStreamWavesPerSimd)))
 void paged_partition_stream_kernel(const DecodeArgs a) {
@@ -1021,6 +1061,13 @@ void paged_partition_stream_kernel(const DecodeArgs a) {
     }
     const int loff = kv_elem_offset(r, 4 * kg);
 
+    // One partial per wave can wait in LDS (this wave's 64-lane slot) for the
+    // end of the wave's range.
+    float* slot = reinterpret_cast<float*>(s_dyn + a.stage_off) +
+                  (static_cast<size_t>(threadIdx.x >> 6) * 64 + lane) * kStageFloats<D>;
+    bool staged = false;
+    PieceDst held{};
+
     int u = u0;
     while (u < u1) {
         // Sequence of block u: the largest s with s_pre[s] <= u. Wave-uniform
@@ -1063,15 +1110,15 @@ void paged_partition_stream_kernel(const DecodeArgs a) {
             const float l_run = sum_over_kg(st.l);
             const float inv = (l_run > 0.0f) ? 1.0f / l_run : 0.0f;
             const bool whole = (seg0 == part * P) && (cut == min(nb, (part + 1) * P));
-            // Wave-uniform bases plus lane byte offsets computed here from
-            // the lane index, so no lane address stays live across the block
-            // loop (the kernel runs at its 168-register cap).
-            int ln = lane;
-            asm volatile("" : "+v"(ln));
-            const int rr = ln & 15;
-            const int kk = ln >> 4;
             const size_t row0 = static_cast<size_t>(s) * a.H + h0;
             if (whole && nparts == 1) {
+                // Lane offsets computed here from the lane index, so no lane
+                // address stays live across the block loop (the kernel runs
+                // at its 168-register cap).
+                int ln = lane;
+                asm volatile("" : "+v"(ln));
+                const int rr = ln & 15;
+                const int kk = ln >> 4;
                 char* ob = pinned_sgpr(reinterpret_cast<char*>(a.out + row0 * D));
                 const unsigned lo = static_cast<unsigned>(rr * D + 4 * kk) * sizeof(f16);
                 if (r < gn) {
@@ -1083,42 +1130,47 @@ void paged_partition_stream_kernel(const DecodeArgs a) {
                         *reinterpret_cast<h4*>(ob + lo + 32u * J) = o;
                     }
                 }
-            } else if (seg0 == part * P) {
-                const size_t p0 = row0 * a.MP + part;
-                char* ob = pinned_sgpr(reinterpret_cast<char*>(a.ws_out + p0 * D));
-                const unsigned lr = static_cast<unsigned>(rr * a.MP) * sizeof(float);
-                const unsigned lo = lr * D + 16u * kk;
-                if (r < gn) {
-#pragma unroll
-                    for (int J = 0; J < NJ; ++J) {
-                        __builtin_nontemporal_store(st.acc[J] * inv, reinterpret_cast<f4*>(ob + lo + 64u * J));
-                    }
-                    if (kk == 0) {
-                        *reinterpret_cast<float*>(pinned_sgpr(reinterpret_cast<char*>(a.ws_max + p0)) + lr) = st.m;
-                        *reinterpret_cast<float*>(pinned_sgpr(reinterpret_cast<char*>(a.ws_sum + p0)) + lr) = l_run;
-                    }
-                }
+                // The compiler treats the wave's memory counter as out of
+                // order while stores and loads are both in flight, and then
+                // waits for every load before each block: a full wait here
+                // keeps the waits in the block loop exact.
+                wait_vm<0>();
             } else {
-                // The piece after a range boundary: only a wave's first piece
-                // can start inside a partition.
-                char* f = pinned_sgpr(reinterpret_cast<char*>(a.frag + static_cast<size_t>(w) * (kFragHead + gstride * D)));
-                const unsigned lo = static_cast<unsigned>(kFragHead + rr * D + 4 * kk) * sizeof(float);
-                if (r < gn) {
+                // A partition slot (the piece starts at its partition's
+                // start) or the wave's boundary slot.
+                PieceDst dst;
+                if (seg0 == part * P) {
+                    const size_t p0 = row0 * a.MP + part;
+                    dst.rows = reinterpret_cast<char*>(a.ws_out + p0 * D);
+                    dst.rstride = static_cast<unsigned>(a.MP) * D * sizeof(float);
+                    dst.m = reinterpret_cast<char*>(a.ws_max + p0);
+                    dst.l = reinterpret_cast<char*>(a.ws_sum + p0);
+                    dst.mstride = static_cast<unsigned>(a.MP) * sizeof(float);
+                } else {
+                    char* f = reinterpret_cast<char*>(a.frag + static_cast<size_t>(w) * (kFragHead + gstride * D));
+                    dst.rows = f + kFragHead * sizeof(float);
+                    dst.rstride = D * sizeof(float);
+                    dst.m = f;
+                    dst.l = f + 16 * sizeof(float);
+                    dst.mstride = sizeof(float);
+                }
+                if (!staged && pre + cut != u1) {
+                    // Held in LDS until the wave's range ends, so that its
+                    // HBM writes do not land among the wave's reads.
 #pragma unroll
-                    for (int J = 0; J < NJ; ++J) {
-                        __builtin_nontemporal_store(st.acc[J] * inv, reinterpret_cast<f4*>(f + lo + 64u * J));
-                    }
-                    if (kk == 0) {
-                        *reinterpret_cast<float*>(f + 4u * rr) = st.m;
-                        *reinterpret_cast<float*>(f + 4u * (16 + rr)) = l_run;
-                    }
+                    for (int J = 0; J < NJ; ++J) *reinterpret_cast<f4*>(slot + 4 * J) = st.acc[J] * inv;
+                    slot[4 * NJ] = st.m;
+                    slot[4 * NJ + 1] = l_run;
+                    held = dst;
+                    staged = true;
+                } else {
+                    f4 v[NJ];
+#pragma unroll
+                    for (int J = 0; J < NJ; ++J) v[J] = st.acc[J] * inv;
+                    write_piece<D>(dst, lane, r < gn, v, st.m, l_run);
+                    wait_vm<0>();
                 }
             }
-            // The compiler treats the wave's memory counter as out of order
-            // while stores and loads are both in flight, and then waits for
-            // every load before each block: a full wait here, once per
-            // partition, keeps the waits in the block loop exact.
-            wait_vm<0>();
             st.m = -INFINITY;
             st.l = 0.0f;
 #pragma unroll
@@ -1127,6 +1179,12 @@ void paged_partition_stream_kernel(const DecodeArgs a) {
             cut = min(j1, cut + P);
         });
         u = pre + j1;
+    }
+    if (staged) {
+        f4 v[NJ];
+#pragma unroll
+        for (int J = 0; J < NJ; ++J) v[J] = *reinterpret_cast<const f4*>(slot + 4 * J);
+        write_piece<D>(held, lane, r < gn, v, slot[4 * NJ], slot[4 * NJ + 1]);
     }
 }
 
@@ -1550,7 +1608,12 @@ int decode_pstream(DecodeArgs& a, char* base, const V2Need& need, const Shape& s
     a.frag = reinterpret_cast<float*>(base + need.frag);
     a.meta = reinterpret_cast<int*>(base + need.meta);
     a.W = need.W;
-    const size_t lds = sizeof(int) * (2 * static_cast<size_t>(sh.S) + 1);
+    // Dynamic LDS: the block prefix and lengths (2S + 1 ints), then every
+    // wave's slot for one held partial (16-byte aligned).
+    a.stage_off = static_cast<int>((2 * static_cast<size_t>(sh.S) + 1 + 3) & ~static_cast<size_t>(3));
+    const size_t stage = static_cast<size_t>(kStreamWaves) * 64 * sizeof(float) *
+                         (sh.D == 128 ? kStageFloats<128> : kStageFloats<64>);
+    const size_t lds = sizeof(int) * static_cast<size_t>(a.stage_off) + stage;
     const dim3 grid(need.W / kStreamWaves);
     hipError_t err = sh.D == 128
         ? launch(paged_partition_stream_kernel<128>, grid, dim3(64 * kStreamWaves), lds, stream, a)
