@@ -892,8 +892,12 @@ __global__ __launch_bounds__(256) void paged_streamk_reduce_kernel(const StreamR
 // goes to the partition's slot of the regular workspace, a piece from a
 // boundary to the boundary slot of wave (t, member) in `frag`. A sequence
 // with one partition and no boundary inside writes its output directly.
-// paged_reduce_pstream_* combine, per head, the partition slots and the
-// boundary slots that fall inside the sequence.
+// The partial of a piece that ends before the wave's range does is held in
+// the wave's LDS slot (one per wave) and written with the wave's last one,
+// so a wave's HBM writes come after its reads instead of among them (writes
+// landing in the read stream cost far more than their bytes).
+// paged_reduce_pstream_wave_kernel combines, per head, the partition slots
+// and the boundary slots that fall inside the sequence.
 // ---------------------------------------------------------------------------
 
 // A wave-uniform pointer held in SGPRs at this point of the program: the
