@@ -105,7 +105,13 @@ void launch_reshape_and_cache(void* key, void* value, void* key_cache,
  * partition and keeps (max logit, exp sum, partial output) in `workspace`;
  * a second kernel rescales and reduces the partitions of every sequence
  * that has more than one (a sequence with a single partition is written by
- * the first kernel directly).
+ * the first kernel directly). For partitions of up to 1024 tokens and at
+ * most a quarter as many sequences as the grid has teams of waves, the
+ * first kernel runs as partition streams: every team of waves takes an
+ * equal range of the batch's blocks and leaves a partial at each partition
+ * end it meets; the workspace then also holds one boundary slot per wave of
+ * the grid, which is sized from the current device's compute units (as is
+ * the size query's answer).
  * partition_size 0 selects balanced scheduling instead: the blocks of all
  * sequences are split into equal ranges, one per team of waves, so a ragged
  * batch has no long tail; ranges that cut a sequence leave fragments that a
