@@ -413,15 +413,17 @@ def test_partition_items_longest_first_cover_every_partition(dev, S, ps):
     assert_attention_close(out[live], _ref(w)[live], f"{S} ragged seqs ps={ps}")
 
 
-@pytest.mark.parametrize("H,Hkv,D", [(64, 8, 128), (64, 2, 128), (32, 8, 64)])
+@pytest.mark.parametrize("H,Hkv,D", [(64, 8, 128), (64, 2, 128), (48, 2, 128), (16, 1, 128), (32, 8, 64)])
 def test_partition_streams_ragged(dev, H, Hkv, D):
     """Split-K over short partitions of a batch with few sequences runs as
     partition streams: equal block ranges per team of waves, cut at partition
     ends and at range boundaries. Ragged contexts with empty sequences put
     range boundaries inside partitions, at partition starts and at sequence
     starts; 16-token partitions make every block a partition, and the 2-kv-head
-    layout (G = 32, two head chunks) gives small teams whose ranges are
-    shorter than a partition."""
+    layouts (G = 32, two head chunks; G = 24, the second chunk 8 heads wide)
+    give small teams whose ranges are shorter than a partition; G = 16 with
+    one kv head gives one-wave teams. Pieces that end inside a wave's range
+    are held in LDS and written with the wave's last piece."""
     rng = np.random.default_rng(H + Hkv + D)
     S = 40
     lens = np.clip(np.rint(np.exp(rng.normal(np.log(1500.0), 1.2, size=S))), 1, 20000).astype(np.int64)
