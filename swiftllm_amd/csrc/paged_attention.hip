@@ -503,7 +503,7 @@ void paged_partition_kernel(const DecodeArgs a) {
 // out[d] = sum_p w_p o_p[d] / sum_p w_p with w_p = exp2(m_p - M) l_p,
 // M = max_p m_p. Accessors: fm(p), fl(p) and fo(p) (pointer to o_p, 8-byte
 // aligned); out(d, v) stores one output.
-// The same combine on one wave: no barriers, lane l owns outputs
+// One wave combines a head: no barriers, lane l owns outputs
 // [l * D / 64, (l + 1) * D / 64), so every fragment row is one coalesced load.
 // The rows of the first CH fragments are loaded before the headers (max and
 // sum) of the first 64, all in flight together, so the combine pays one
@@ -581,8 +581,9 @@ __device__ __forceinline__ void combine_head_wave(int P, FM fm, FL fl, FO fo, OU
 // fragments, else 64 (128 registers of rows at D = 128).
 constexpr int kReduceSmall = 16;
 
-// Split-K reduce: one workgroup per (query head, sequence); sequences with a
-// single partition were written directly by the partition kernel.
+// Split-K reduce of the partition kernel: one wave per (query head,
+// sequence); sequences with a single partition were written directly by the
+// partition kernel.
 struct ReduceArgs {
     f16* out;
     const int* ctx;
@@ -616,7 +617,6 @@ __global__ __launch_bounds__(256) void paged_reduce_wave_kernel(const ReduceArgs
         [&](int p) { return po + static_cast<size_t>(p) * D; },
         [&](int d, float v) { o[d] = static_cast<f16>(v); });
 }
-
 
 // ---------------------------------------------------------------------------
 // Balanced ("stream-K") decode. The blocks of all sequences form one list,
