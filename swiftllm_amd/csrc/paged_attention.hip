@@ -581,6 +581,83 @@ __device__ __forceinline__ void combine_head_wave(int P, FM fm, FL fl, FO fo, OU
 // fragments, else 64 (128 registers of rows at D = 128).
 constexpr int kReduceSmall = 16;
 
+// The same combine by the NW waves of a workgroup, for heads with many
+// fragments: wave w takes the 16-fragment chunks w, w + NW, ..., keeping a
+// running max, sum and rescaled partial over its chunks (one memory latency
+// per chunk, its 16 rows loaded before the headers), and wave 0 merges the
+// NW partials through LDS. A head then costs ceil(P / (16 NW)) latencies
+// instead of ceil(P / 64), with NW times the waves in flight.
+template <int D, int NW, typename FM, typename FL, typename FO, typename OUT>
+__device__ __forceinline__ void combine_head_split(int P, FM fm, FL fl, FO fo, OUT out) {
+    constexpr int DL = D / 64;
+    constexpr int CH = 16;
+    __shared__ float s_acc[NW][D];
+    __shared__ float s_md[NW][2];
+    const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    if (P <= 0) {
+        if (wv == 0) {
+#pragma unroll
+            for (int j = 0; j < DL; ++j) out(lane * DL + j, 0.0f);
+        }
+        return;
+    }
+    float M = -INFINITY;
+    float den = 0.0f;
+    float acc[DL];
+#pragma unroll
+    for (int j = 0; j < DL; ++j) acc[j] = 0.0f;
+    for (int c0 = wv * CH; c0 < P; c0 += NW * CH) {
+        float v[CH][DL];
+#pragma unroll
+        for (int i = 0; i < CH; ++i) load_row<D>(fo(min(c0 + i, P - 1)) + lane * DL, v[i]);
+        const int p = c0 + lane;
+        const bool mine = lane < CH && p < P;
+        const float mp = mine ? fm(p) : -INFINITY;
+        const float lp = mine ? fl(p) : 0.0f;
+        const float Mn = fmaxf(M, wave_max(mp));
+        if (Mn == -INFINITY) continue;  // every fragment so far empty (wave-uniform)
+        const float sc = (M == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(M - Mn);
+        const float w = (mp == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mp - Mn) * lp;
+        den = den * sc + wave_sum(w);
+#pragma unroll
+        for (int j = 0; j < DL; ++j) acc[j] *= sc;
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const float wi = readlane_f(w, i);
+#pragma unroll
+            for (int j = 0; j < DL; ++j) acc[j] += wi * v[i][j];
+        }
+        M = Mn;
+    }
+#pragma unroll
+    for (int j = 0; j < DL; ++j) s_acc[wv][lane * DL + j] = acc[j];
+    if (lane == 0) {
+        s_md[wv][0] = M;
+        s_md[wv][1] = den;
+    }
+    __syncthreads();
+    if (wv != 0) return;
+    float Mall = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) Mall = fmaxf(Mall, s_md[w][0]);
+    float tot[DL];
+#pragma unroll
+    for (int j = 0; j < DL; ++j) tot[j] = 0.0f;
+    float dall = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        const float Mw = s_md[w][0];
+        const float f = (Mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(Mw - Mall);
+        dall += f * s_md[w][1];
+#pragma unroll
+        for (int j = 0; j < DL; ++j) tot[j] += f * s_acc[w][lane * DL + j];
+    }
+    const float inv = dall > 0.0f ? 1.0f / dall : 0.0f;
+#pragma unroll
+    for (int j = 0; j < DL; ++j) out(lane * DL + j, tot[j] * inv);
+}
+
 // Split-K reduce of the partition kernel: one wave per (query head,
 // sequence); sequences with a single partition were written directly by the
 // partition kernel.
@@ -896,8 +973,10 @@ __global__ __launch_bounds__(256) void paged_streamk_reduce_kernel(const StreamR
 // the wave's LDS slot (one per wave) and written with the wave's last one,
 // so a wave's HBM writes come after its reads instead of among them (writes
 // landing in the read stream cost far more than their bytes).
-// paged_reduce_pstream_wave_kernel combines, per head, the partition slots
-// and the boundary slots that fall inside the sequence.
+// paged_reduce_pstream_wave_kernel (up to 16 fragments per head, a wave per
+// head) and paged_reduce_pstream_split_kernel (more, four waves per head)
+// combine, per head, the partition slots and the boundary slots that fall
+// inside the sequence.
 // ---------------------------------------------------------------------------
 
 // A wave-uniform pointer held in SGPRs at this point of the program: the
@@ -1207,6 +1286,8 @@ struct PStreamReduceArgs {
     int H, G, nhc, MP, part_blocks, gstride, TS;
 };
 
+// CH: fragment rows per batch of the one-wave combine; 0: the head is
+// combined by the four waves of the workgroup (combine_head_split).
 template <int D, int CH>
 __device__ __forceinline__ void pstream_reduce_head(const PStreamReduceArgs& a, int s, int h) {
     const int q = a.meta[0];
@@ -1254,7 +1335,11 @@ __device__ __forceinline__ void pstream_reduce_head(const PStreamReduceArgs& a, 
     };
     f16* o = a.out + row * D;
     auto out = [&](int d, float v) { o[d] = static_cast<f16>(v); };
-    combine_head_wave<D, CH>(nparts + nbound, fm, fl, fo, out);
+    if constexpr (CH == 0) {
+        combine_head_split<D, 4>(nparts + nbound, fm, fl, fo, out);
+    } else {
+        combine_head_wave<D, CH>(nparts + nbound, fm, fl, fo, out);
+    }
 }
 
 template <int D, int CH>
@@ -1262,6 +1347,12 @@ __global__ __launch_bounds__(256) void paged_reduce_pstream_wave_kernel(const PS
     const int h = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (h >= a.H) return;
     pstream_reduce_head<D, CH>(a, blockIdx.y, h);
+}
+
+// One (query head, sequence) per workgroup of four waves.
+template <int D>
+__global__ __launch_bounds__(256) void paged_reduce_pstream_split_kernel(const PStreamReduceArgs a) {
+    pstream_reduce_head<D, 0>(a, blockIdx.y, blockIdx.x);
 }
 
 // Bit-exact materialisation of one (sequence, kv head) through the tile
@@ -1644,8 +1735,9 @@ int decode_pstream(DecodeArgs& a, char* base, const V2Need& need, const Shape& s
         err = sh.D == 128 ? launch(paged_reduce_pstream_wave_kernel<128, kReduceSmall>, rgrid, dim3(256), 0, stream, r)
                           : launch(paged_reduce_pstream_wave_kernel<64, kReduceSmall>, rgrid, dim3(256), 0, stream, r);
     } else {
-        err = sh.D == 128 ? launch(paged_reduce_pstream_wave_kernel<128, 64>, rgrid, dim3(256), 0, stream, r)
-                          : launch(paged_reduce_pstream_wave_kernel<64, 64>, rgrid, dim3(256), 0, stream, r);
+        const dim3 sgrid(a.H, sh.S);
+        err = sh.D == 128 ? launch(paged_reduce_pstream_split_kernel<128>, sgrid, dim3(256), 0, stream, r)
+                          : launch(paged_reduce_pstream_split_kernel<64>, sgrid, dim3(256), 0, stream, r);
     }
     return launched(err, who);
 }
