@@ -20,8 +20,8 @@
 // (2048 at D 128, BS 16), past the 1024-thread limit, so its launch fails.
 // Here one kernel moves every (pair, array, chunk) in one launch: a
 // workgroup moves a chunk of about 16 KiB with 16-byte accesses, four loads
-// per thread in flight before the stores, which are nontemporal (the copy is
-// not read back by this kernel). Pinned host memory is addressed directly by
+// per thread in flight before the stores. Loads and stores are nontemporal:
+// each byte is read once and the copy is not read back by this kernel. Pinned host memory is addressed directly by
 // the kernel, so a swap in either direction is one launch instead of one DMA
 // request per block.
 
@@ -72,7 +72,7 @@ __global__ __launch_bounds__(kCopyThreads) void block_copy_kernel(const BlockCop
 #pragma unroll
             for (int u = 0; u < kCopyUnroll; ++u) {
                 const size_t i = i0 + static_cast<size_t>(u) * kCopyThreads;
-                if (i < v1) v[u] = sv[i];
+                if (i < v1) v[u] = __builtin_nontemporal_load(sv + i);
             }
 #pragma unroll
             for (int u = 0; u < kCopyUnroll; ++u) {

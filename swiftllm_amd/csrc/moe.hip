@@ -25,9 +25,10 @@
 //               Then one wave per token computes the K destination rows,
 //               writes the inverse index and sorted token ids, and copies the
 //               token's row once from HBM into its K destinations, every load
-//               of a batch issued before its stores. The destination rows are
-//               written with nontemporal stores (measured faster than plain
-//               ones for this one-read, K-write pattern).
+//               of a batch issued before its stores. Rows are read with
+//               nontemporal loads and written with nontemporal stores (both
+//               measured faster than plain ones for this one-read, K-write
+//               pattern).
 //           Larger count matrices get a scan kernel between the two: one
 //           workgroup per expert turns its column into exclusive prefixes
 //           and the expert's total.
@@ -420,7 +421,7 @@ __global__ __launch_bounds__(64 * kPermuteWaves) void moe_permute_kernel(const P
     u32x4 v[kCopyBatch];
     if constexpr (VEC) {
 #pragma unroll
-        for (int u = 0; u < kCopyBatch; ++u) v[u] = src[min(64 * u + lane, nv - 1)];
+        for (int u = 0; u < kCopyBatch; ++u) v[u] = __builtin_nontemporal_load(src + min(64 * u + lane, nv - 1));
     }
 
     // Per-expert totals: from the scan kernel, or scanned here from the counts.
@@ -493,7 +494,7 @@ __global__ __launch_bounds__(64 * kPermuteWaves) void moe_permute_kernel(const P
 #pragma unroll
                 for (int u = 0; u < kCopyBatch; ++u) {
                     const int i = i0 + 64 * u + lane;
-                    if (i < nv) v[u] = src[i];
+                    if (i < nv) v[u] = __builtin_nontemporal_load(src + i);
                 }
             }
 #pragma unroll

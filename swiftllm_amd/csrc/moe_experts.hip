@@ -54,6 +54,9 @@ constexpr int kAStages = 2;     // LDS buffers of the activation tile
 constexpr int kWStages = 3;     // LDS buffers of the weight tile (its lines miss L2 more)
 constexpr int kThreads = 512;   // 8 waves: 2 (rows) x 4 (weight rows), 128 x 64 each
 constexpr int kRowChunks = kBK / 8;                        // 16-byte chunks per tile row
+// Cache policy of a buffer load: the nt bit (streaming), for the thin
+// kernel's weight rows, which it reads once per call.
+constexpr int kNontemporal = 2;
 constexpr int kTileChunks = kBM * kRowChunks;              // chunks per operand tile
 constexpr size_t kTileHalfs = static_cast<size_t>(kBM) * kBK;  // one operand tile of a stage
 static_assert(kBM == kBW, "activation and weight tiles share one LDS buffer size");
@@ -431,14 +434,23 @@ __device__ __forceinline__ void thin_issue(f16* lds, __amdgpu_buffer_rsrc_t rx, 
                                            __amdgpu_buffer_rsrc_t rw2, const unsigned* off, int wv,
                                            int ks, int buf) {
     using C = Thin<GATED, NTT>;
+    static_assert((C::TW * kRowChunks) % kThinThreads == 0 && (C::OUT * kRowChunks) % kThinThreads == 0,
+                  "the rows of load j lie in one operand for every wave");
     const unsigned soff = static_cast<unsigned>(ks) * kBK * 2u;
 #pragma unroll
     for (int j = 0; j < C::L; ++j) {
-        const int r = (j * kThinThreads + wv * 64) / kRowChunks;   // first row of the load
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            r >= C::TW ? rx : ((GATED && r >= C::OUT) ? rw2 : rw),
-            to_lds(lds + static_cast<size_t>(buf) * C::SH + (j * kThinThreads + wv * 64) * 8), 16,
-            off[j], soff, 0, 0);
+        // Load j of every wave reads rows of one operand (rj: its first row
+        // for wave 0), so the choice below is made at compile time. The
+        // weight rows are read once per call and go nontemporal; the tail
+        // rows, which every column tile of the expert reads, stay cached.
+        const int rj = j * kThinThreads / kRowChunks;
+        f16* dst = lds + static_cast<size_t>(buf) * C::SH + (j * kThinThreads + wv * 64) * 8;
+        if (rj >= C::TW) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, to_lds(dst), 16, off[j], soff, 0, 0);
+        } else {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds((GATED && rj >= C::OUT) ? rw2 : rw, to_lds(dst), 16,
+                                                     off[j], soff, 0, kNontemporal);
+        }
     }
 }
 
