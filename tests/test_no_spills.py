@@ -8,7 +8,9 @@ for it (a 13-register spill in the partition kernel cost 26 us on config 3 and
 config 4 alike), while the results stay correct and no GPU test notices. The
 one allowance: the D = 128 prefill kernels with K through LDS spill 4
 registers at 256 VGPRs, a measured trade (one wave per SIMD without the spill
-ran slower).
+ran slower). Their spill stores and reloads must lie outside every loop of
+the kernel (the compiler marks loop blocks "in Loop"), so the key walk itself
+never touches scratch; they sit in the peeled last steps.
 """
 
 import re
@@ -32,6 +34,21 @@ def _device_sources():
     return [s for s in build.SOURCES if s.endswith(".hip")]
 
 
+def _scratch_ops(text, name):
+    """(instruction, inside a loop) for every scratch access of kernel `name`."""
+    start = text.index(f"\n{name}:")
+    end = text.index(".Lfunc_end", start)
+    in_loop, ops, loops = False, [], 0
+    for line in text[start:end].splitlines()[1:]:
+        s = line.strip()
+        if re.match(r"^(\.LBB\d+_\d+:|; %bb\.\d+:)", s):
+            in_loop = "in Loop" in s
+            loops += in_loop
+        elif s.startswith("scratch_"):
+            ops.append((s, in_loop))
+    return ops, loops
+
+
 @pytest.mark.parametrize("src", _device_sources())
 def test_no_vgpr_spills(src, tmp_path):
     if not Path(HIPCC).exists() and shutil.which("hipcc") is None:
@@ -49,3 +66,9 @@ def test_no_vgpr_spills(src, tmp_path):
     for name, n in zip(names, spills):
         allowed = next((v for k, v in ALLOWED.items() if name.startswith(k)), 0)
         assert n <= allowed, f"{src}: {name} spills {n} VGPRs (allowed {allowed})"
+        if n > 0:
+            ops, loops = _scratch_ops(text, name)
+            assert loops > 0, f"{src}: {name}: no loop blocks found"
+            assert ops, f"{src}: {name}: spills but no scratch access found"
+            inside = [op for op, in_loop in ops if in_loop]
+            assert not inside, f"{src}: {name} touches scratch inside a loop: {inside}"
