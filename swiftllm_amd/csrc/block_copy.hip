@@ -21,9 +21,9 @@
 // Here one kernel moves every (pair, array, chunk) in one launch: a
 // workgroup moves a chunk of about 16 KiB with 16-byte accesses, four loads
 // per thread in flight before the stores. Loads and stores are nontemporal:
-// each byte is read once and the copy is not read back by this kernel. Pinned host memory is addressed directly by
-// the kernel, so a swap in either direction is one launch instead of one DMA
-// request per block.
+// each byte is read once and the copy is not read back by this kernel.
+// Pinned host memory is addressed directly by the kernel, so a swap in
+// either direction is one launch instead of one DMA request per block.
 
 #include "common.hpp"
 
