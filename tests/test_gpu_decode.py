@@ -436,3 +436,24 @@ def test_partition_streams_ragged(dev, H, Hkv, D):
         out = dw.run("v2", partition_size=ps)
         assert np.all(out[~live] == 0), f"ps={ps}: empty sequences must be zero"
         assert_attention_close(out[live], ref[live], f"streams H{H} Hkv{Hkv} D{D} ps={ps}")
+
+
+@pytest.mark.parametrize("D", [128, 64])
+def test_partition_stream_reduce_fragment_counts(dev, D):
+    """The reduce of a head with more than 16 fragments runs on four waves,
+    each combining 16-fragment chunks, merged through LDS. With 16-token
+    partitions every block is a partition and every range boundary falls on a
+    partition start, so a sequence of n blocks leaves exactly n fragments per
+    head. The counts cross a wave's chunk (16 / 17), one pass of the four
+    waves (63 / 64 / 65) and several passes (129, 200), beside sequences of 1
+    block (written directly), 2 and 8 blocks and an empty one; some last
+    blocks are partial."""
+    rng = np.random.default_rng(77 + D)
+    blocks = np.array([1, 2, 8, 9, 16, 17, 63, 64, 65, 129, 200, 0])
+    lens = blocks * 16 - (np.arange(len(blocks)) % 3) * 5
+    lens[blocks == 0] = 0
+    w = _random_batch(rng, lens, H=64, Hkv=8, D=D)
+    out = DeviceWorkload(w).run("v2", partition_size=16)
+    live = lens > 0
+    assert np.all(out[~live] == 0), "empty sequences must be zero"
+    assert_attention_close(out[live], _ref(w)[live], f"reduce fragment counts D{D}")
