@@ -673,13 +673,10 @@ struct ReduceArgs {
     int MP;
 };
 
-// One wave per (query head, sequence), four heads per workgroup; CH fragment
-// rows per load batch.
+// Combine of head h of sequence s; CH: fragment rows per load batch of the
+// one-wave combine, 0: the four waves of the workgroup (combine_head_split).
 template <int D, int CH>
-__global__ __launch_bounds__(256) void paged_reduce_wave_kernel(const ReduceArgs a) {
-    const int h = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int s = blockIdx.y;
-    if (h >= a.H) return;
+__device__ __forceinline__ void reduce_head(const ReduceArgs& a, int s, int h) {
     const int L = max(a.ctx[s], 0);
     const int nblk = min((L + kBlockTokens - 1) / kBlockTokens, a.MB);
     const int nparts = (nblk + a.part_blocks - 1) / a.part_blocks;
@@ -689,10 +686,31 @@ __global__ __launch_bounds__(256) void paged_reduce_wave_kernel(const ReduceArgs
     const float* pl = a.ws_sum + row * a.MP;
     const float* po = a.ws_out + row * a.MP * D;
     f16* o = a.out + row * D;
-    combine_head_wave<D, CH>(
-        nparts, [&](int p) { return pm[p]; }, [&](int p) { return pl[p]; },
-        [&](int p) { return po + static_cast<size_t>(p) * D; },
-        [&](int d, float v) { o[d] = static_cast<f16>(v); });
+    auto fm = [&](int p) { return pm[p]; };
+    auto fl = [&](int p) { return pl[p]; };
+    auto fo = [&](int p) { return po + static_cast<size_t>(p) * D; };
+    auto out = [&](int d, float v) { o[d] = static_cast<f16>(v); };
+    if constexpr (CH == 0) {
+        combine_head_split<D, 4>(nparts, fm, fl, fo, out);
+    } else {
+        combine_head_wave<D, CH>(nparts, fm, fl, fo, out);
+    }
+}
+
+// One wave per (query head, sequence), four heads per workgroup; CH fragment
+// rows per load batch.
+template <int D, int CH>
+__global__ __launch_bounds__(256) void paged_reduce_wave_kernel(const ReduceArgs a) {
+    const int h = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (h >= a.H) return;
+    reduce_head<D, CH>(a, blockIdx.y, h);
+}
+
+// One (query head, sequence) per workgroup of four waves, for more than 16
+// partitions per sequence.
+template <int D>
+__global__ __launch_bounds__(256) void paged_reduce_split_kernel(const ReduceArgs a) {
+    reduce_head<D, 0>(a, blockIdx.y, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -1579,13 +1597,14 @@ V2Need v2_need(const Shape& sh, int partition_size, int cus) {
     return n;
 }
 
-// A wave combines a head: row batches of kReduceSmall for up to that many
-// partitions per sequence, else of 64.
+// A wave combines a head in one batch of kReduceSmall rows for up to that
+// many partitions per sequence; beyond, the four waves of a workgroup do.
 template <int D>
 hipError_t launch_reduce_t(const ReduceArgs& r, int S, hipStream_t stream) {
-    const dim3 grid((r.H + 3) / 4, S);
-    if (r.MP <= kReduceSmall) return launch(paged_reduce_wave_kernel<D, kReduceSmall>, grid, dim3(256), 0, stream, r);
-    return launch(paged_reduce_wave_kernel<D, 64>, grid, dim3(256), 0, stream, r);
+    if (r.MP <= kReduceSmall) {
+        return launch(paged_reduce_wave_kernel<D, kReduceSmall>, dim3((r.H + 3) / 4, S), dim3(256), 0, stream, r);
+    }
+    return launch(paged_reduce_split_kernel<D>, dim3(r.H, S), dim3(256), 0, stream, r);
 }
 
 int validate_partition(const char* who, int partition_size) {

@@ -439,6 +439,26 @@ def test_partition_streams_ragged(dev, H, Hkv, D):
 
 
 @pytest.mark.parametrize("D", [128, 64])
+def test_item_reduce_many_partitions(dev, D):
+    """Split-K over the item kernel (80 sequences: more than a quarter of the
+    teams a partition stream needs) with up to 188 partitions per sequence:
+    above 16 partitions the reduce runs on four waves per head (16, 64), at
+    most 16 on one wave (256); empty and one-block sequences included."""
+    rng = np.random.default_rng(91 + D)
+    S = 80
+    lens = np.clip(np.rint(np.exp(rng.normal(np.log(700.0), 1.0, size=S))), 1, 3000).astype(np.int64)
+    lens[:3] = [0, 1, 3000]
+    w = _random_batch(rng, lens, H=32, Hkv=8, D=D)
+    dw = DeviceWorkload(w)
+    ref = _ref(w)
+    live = lens > 0
+    for ps in (16, 64, 256):
+        out = dw.run("v2", partition_size=ps)
+        assert np.all(out[~live] == 0), f"ps={ps}: empty sequences must be zero"
+        assert_attention_close(out[live], ref[live], f"item reduce D{D} ps={ps}")
+
+
+@pytest.mark.parametrize("D", [128, 64])
 def test_partition_stream_reduce_fragment_counts(dev, D):
     """The reduce of a head with more than 16 fragments runs on four waves,
     each combining 16-fragment chunks, merged through LDS. With 16-token
