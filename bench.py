@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the paged-attention decode hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1..9]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1..10]
                     [--variant v2|v1] [--partition P] [--rotate R] [--no-cpu]
                     [--no-ceiling] [--ceiling stream|gather|store|rowcopy]
 
@@ -28,11 +28,14 @@ claim), --config 3 (8 sequences of 32768 tokens, 64 query heads, split-K),
 experts), and the "next" rows: --config 6/7 (block copies and swaps), 8 (the
 Mixtral MoE layer's expert GEMMs), 9 (paged prefill) and 10 (the same MoE
 layer at a 64-token decode batch, where the expert GEMMs stream weights).
+With no --config the line is config 2's and carries every other config as a
+sub-record under "configs", each timed in the same process on its own inputs.
 """
 
 from __future__ import annotations
 
 import argparse
+import copy
 import json
 import os
 import sys
@@ -94,7 +97,7 @@ def parse():
                     help="config 3: do not also time 4096-token partitions beside BASELINE's 512 (for "
                          "profiles whose per-kernel averages should cover the main workload only)")
     ap.add_argument("--no-configs", action="store_true",
-                    help="config 2: leave out the sub-records of configs 1, 3, 4 and 5 that the default "
+                    help="config 2: leave out the sub-records of configs 1 and 3-10 that the default "
                          "line carries (for profiles of config 2 alone)")
     ap.add_argument("--kernel", default=None, help="kernel name substring for --summarize-pmc")
     ap.add_argument("--alg-bytes", type=int, default=0,
@@ -212,14 +215,11 @@ def main():
     if args.config == 5:
         print(json.dumps(bench_moe(args)), flush=True)
         return
-    if args.config in (6, 7):
-        return bench_blocks(args)
-    if args.config == 8:
-        return bench_moe_mlp(args)
-    if args.config == 9:
-        return bench_prefill(args)
-    if args.config == 10:
-        return bench_moe_decode(args)
+    single = {6: bench_blocks, 7: bench_blocks, 8: bench_moe_mlp, 9: bench_prefill,
+              10: bench_moe_decode}
+    if args.config in single:
+        print(json.dumps(single[args.config](args)), flush=True)
+        return
     rec = bench_decode(args, args.config, variant=args.variant, partition=args.partition)
     if args.config == 2 and not args.no_configs:
         rec["configs"] = other_configs(args, rec)
@@ -461,19 +461,34 @@ _SUB_DROP = ("n_gpus", "scaling", "vs_baseline", "higher_is_better", "steps", "w
 
 
 def other_configs(args, main_rec):
-    """BASELINE configs 1, 3, 4 and 5, each on its own seeded inputs, timed in
-    this process after the headline config 2, as sub-records of its line:
-    us/call, the roofline of the algorithmic bytes against 8 TB/s with the
-    committed HBM traffic, the live ceiling of the call's own access pattern,
-    and the CPU restatement on this host. Config 3 runs at BASELINE's
-    512-token partitions, with 4096-token partitions timed beside it."""
+    """Every other config, each on its own seeded inputs, timed in this
+    process after the headline config 2, as sub-records of its line.
+    BASELINE configs 1, 3, 4 and 5: us/call, the roofline of the algorithmic
+    bytes against 8 TB/s with the committed HBM traffic, the live ceiling of
+    the call's own access pattern, and the CPU restatement on this host
+    (config 3 at BASELINE's 512-token partitions, with 4096-token partitions
+    timed beside it). Configs 6-10 (block copies, the MoE layer at 4096 and
+    64 tokens, paged prefill): their own records without a CPU leg. A config
+    that fails records its error instead, so the headline line is printed
+    whatever happens to the others."""
     stream_gbs = main_rec.get("stream_read_gbs")
+    single = {6: bench_blocks, 7: bench_blocks, 8: bench_moe_mlp, 9: bench_prefill,
+              10: bench_moe_decode}
     subs = {}
-    for cfg in (1, 3, 4, 5):
-        if cfg == 5:
-            rec = bench_moe(args, stream_gbs=stream_gbs, log_prefix="[bench]")
-        else:
-            rec = bench_decode(args, cfg, stream_gbs=stream_gbs)
+    for cfg in (1, 3, 4, 5, 6, 7, 8, 9, 10):
+        try:
+            if cfg == 5:
+                rec = bench_moe(args, stream_gbs=stream_gbs, log_prefix="[bench]")
+            elif cfg in single:
+                sub_args = copy.copy(args)
+                sub_args.config = cfg
+                rec = single[cfg](sub_args)
+            else:
+                rec = bench_decode(args, cfg, stream_gbs=stream_gbs)
+        except Exception as e:  # recorded, so that the headline still prints
+            print(f"[bench] config {cfg} failed: {e!r}", file=sys.stderr, flush=True)
+            subs[str(cfg)] = {"error": repr(e)}
+            continue
         rec["steps_timed"] = rec.get("steps")
         subs[str(cfg)] = {k: v for k, v in rec.items() if k not in _SUB_DROP}
     return subs
@@ -886,7 +901,7 @@ def bench_prefill(args):
     ceiling = mfma_ceiling(stream, args.no_ceiling)
     rec["ceiling"] = ceiling
     rec["ceiling_frac"] = round(tflops / ceiling["value"], 4) if ceiling else None
-    print(json.dumps(rec), flush=True)
+    return rec
 
 
 def bench_moe_decode(args):
@@ -951,7 +966,7 @@ def bench_moe_decode(args):
         "ceiling_frac": round(value / stream_gbs, 4) if stream_gbs else None,
         "cpu_baseline": None,
     }
-    print(json.dumps(rec), flush=True)
+    return rec
 
 
 def bench_moe_mlp(args):
@@ -1004,7 +1019,7 @@ def bench_moe_mlp(args):
     ceiling = mfma_ceiling(stream, args.no_ceiling)
     rec["ceiling"] = ceiling
     rec["ceiling_frac"] = round(tflops / ceiling["value"], 4) if ceiling else None
-    print(json.dumps(rec), flush=True)
+    return rec
 
 
 def bench_blocks(args):
@@ -1077,7 +1092,7 @@ def bench_blocks(args):
                          frac=round(value / roof["peak"], 4), traffic=None),
         "cpu_baseline": None,
     }
-    print(json.dumps(rec), flush=True)
+    return rec
 
 
 if __name__ == "__main__":
