@@ -58,3 +58,52 @@ def test_summarize_pmc_scales_by_the_calibration_copy(tmp_path):
     assert rec["dispatches_averaged"] == 2
     assert rec["other_kernels_same_call"] == {"other(B)": {"fetch_kib": 7.0, "write_kib": 0.0}}
     assert rec["algorithmic_bytes_per_launch"] == 4096000
+
+
+def test_default_line_sub_records_cover_every_config(monkeypatch):
+    """The default line's sub-records: configs 1 and 3-10 in one pass, the
+    block-copy and MoE/prefill benches called with their own config number,
+    and a config that raises recorded as an error instead of ending the run
+    (no GPU: the bench functions are stand-ins)."""
+    import argparse
+
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    seen = []
+
+    def rec(cfg):
+        return {"us_per_call": float(cfg), "steps": 7, "n_gpus": 1}
+
+    def decode(args, cfg, stream_gbs=None):
+        seen.append(("decode", cfg))
+        return rec(cfg)
+
+    def moe(args, stream_gbs=None, log_prefix=""):
+        seen.append(("moe", 5))
+        return rec(5)
+
+    def single(name):
+        def run(args):
+            seen.append((name, args.config))
+            if args.config == 9:
+                raise RuntimeError("planted failure")
+            return rec(args.config)
+        return run
+
+    monkeypatch.setattr(bench, "bench_decode", decode)
+    monkeypatch.setattr(bench, "bench_moe", moe)
+    monkeypatch.setattr(bench, "bench_blocks", single("blocks"))
+    monkeypatch.setattr(bench, "bench_moe_mlp", single("mlp"))
+    monkeypatch.setattr(bench, "bench_prefill", single("prefill"))
+    monkeypatch.setattr(bench, "bench_moe_decode", single("moe_decode"))
+    args = argparse.Namespace(config=2, steps=7)
+    subs = bench.other_configs(args, {"stream_read_gbs": None})
+    assert sorted(subs, key=int) == ["1", "3", "4", "5", "6", "7", "8", "9", "10"]
+    assert seen == [("decode", 1), ("decode", 3), ("decode", 4), ("moe", 5), ("blocks", 6),
+                    ("blocks", 7), ("mlp", 8), ("prefill", 9), ("moe_decode", 10)]
+    assert args.config == 2, "the headline's arguments are left as they were"
+    assert subs["9"] == {"error": "RuntimeError('planted failure')"}
+    for k in ("1", "3", "4", "5", "6", "7", "8", "10"):
+        assert subs[k]["us_per_call"] == float(k) and subs[k]["steps_timed"] == 7
+        assert "n_gpus" not in subs[k] and "steps" not in subs[k]
